@@ -1,0 +1,577 @@
+// C ABI entry points: context, errors, attention calls, device KvCache, the
+// layer attention driver, the engine's policies and the ComputePort methods.
+
+#include <math.h>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "g4_internal.h"
+
+namespace {
+
+thread_local std::string t_msg;
+thread_local uint64_t t_field_a = 0, t_field_b = 0;
+
+hipStream_t as_stream(g4_stream s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Runs `body`, turning any escaping C++ exception into an error code.
+template <class F>
+int guarded(F &&body) {
+    try {
+        return body();
+    } catch (const std::bad_alloc &) {
+        return g4::set_error(G4_ERR_COMPUTE, "host allocation failed");
+    } catch (...) {
+        return g4::set_error(G4_ERR_COMPUTE, "unexpected internal error");
+    }
+}
+
+int invalid(const char *what) { return g4::set_error(G4_ERR_COMPUTE, what); }
+
+}  // namespace
+
+namespace g4 {
+
+int set_error(int code, const std::string &message, uint64_t a, uint64_t b) {
+    t_msg = message;
+    t_field_a = a;
+    t_field_b = b;
+    return code;
+}
+
+void clear_error() {
+    t_msg.clear();
+    t_field_a = t_field_b = 0;
+}
+
+int hip_failed(hipError_t e, const char *what) {
+    return set_error(G4_ERR_COMPUTE, std::string("hip: ") + hipGetErrorString(e) + " (" + what + ")");
+}
+
+int ensure_workspace(g4_ctx *ctx, size_t bytes, hipStream_t stream) {
+    (void)stream;
+    if (ctx->ws.bytes >= bytes) return G4_OK;
+    // Growth is rare (first use of a larger shape): drain all work that may
+    // still read the old buffer before replacing it.
+    G4_HIP(hipDeviceSynchronize());
+    if (ctx->ws.ptr) G4_HIP(hipFree(ctx->ws.ptr));
+    ctx->ws.ptr = nullptr;
+    ctx->ws.bytes = 0;
+    const size_t grown = bytes + bytes / 4;
+    G4_HIP(hipMalloc(&ctx->ws.ptr, grown));
+    ctx->ws.bytes = grown;
+    return G4_OK;
+}
+
+}  // namespace g4
+
+// -------------------------------------------------------------- device KvCache
+struct g4_kv_cache {
+    g4_ctx *ctx = nullptr;
+    int n_layers = 0;
+    int64_t capacity = 0;
+    std::vector<int64_t> width;
+    std::vector<float *> k, v;
+    std::vector<int64_t> rows;
+    int known_layers = 0;  // layers.len() of the reference's Vec<Layer>
+};
+
+extern "C" {
+
+const char *g4_last_error(void) { return t_msg.c_str(); }
+
+void g4_last_error_fields(uint64_t *a, uint64_t *b) {
+    if (a) *a = t_field_a;
+    if (b) *b = t_field_b;
+}
+
+int g4_init(int device, g4_ctx **out) {
+    return guarded([&] {
+        g4::clear_error();
+        if (!out) return invalid("g4_init: null output pointer");
+        *out = nullptr;
+        G4_HIP(hipSetDevice(device));
+        auto *ctx = new g4_ctx();
+        ctx->device = device;
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && cus > 0)
+            ctx->num_cus = cus;
+        hipError_t e = hipMalloc(&ctx->status_dev, sizeof(unsigned));
+        if (e == hipSuccess) e = hipMemset(ctx->status_dev, 0, sizeof(unsigned));
+        if (e != hipSuccess) {
+            if (ctx->status_dev) (void)hipFree(ctx->status_dev);
+            delete ctx;
+            return g4::hip_failed(e, "g4_init");
+        }
+        *out = ctx;
+        return (int)G4_OK;
+    });
+}
+
+int g4_release(g4_ctx *ctx) {
+    return guarded([&] {
+        if (!ctx) return (int)G4_OK;
+        G4_HIP(hipSetDevice(ctx->device));
+        G4_HIP(hipDeviceSynchronize());
+        if (ctx->ws.ptr) G4_HIP(hipFree(ctx->ws.ptr));
+        if (ctx->status_dev) G4_HIP(hipFree(ctx->status_dev));
+        delete ctx;
+        return (int)G4_OK;
+    });
+}
+
+int g4_check_status(g4_ctx *ctx, g4_stream stream) {
+    return guarded([&] {
+        if (!ctx) return invalid("g4_check_status: null context");
+        G4_HIP(hipStreamSynchronize(as_stream(stream)));
+        unsigned st = 0;
+        G4_HIP(hipMemcpy(&st, ctx->status_dev, sizeof st, hipMemcpyDeviceToHost));
+        if (st == 0) return (int)G4_OK;
+        G4_HIP(hipMemset(ctx->status_dev, 0, sizeof(unsigned)));
+        if (st & g4::kStatusNonFinite)
+            return g4::set_error(G4_ERR_COMPUTE, "softmax input is not finite");
+        return g4::set_error(G4_ERR_CONTEXT_TOO_LONG,
+                             "a sequence's K/V range is longer than max_kv_len");
+    });
+}
+
+int g4_set_decode_chunk(g4_ctx *ctx, int64_t keys) {
+    if (!ctx) return invalid("g4_set_decode_chunk: null context");
+    if (keys < 0) return invalid("g4_set_decode_chunk: negative key count");
+    ctx->decode_chunk = keys;
+    return G4_OK;
+}
+
+// ------------------------------------------------------------------ attention
+static int check_heads(int n_heads, int n_kv_heads, int head_dim) {
+    if (n_heads <= 0 || n_kv_heads <= 0 || head_dim <= 0)
+        return invalid("attention needs positive head counts and head width");
+    if (n_kv_heads > n_heads) return invalid("more KV heads than query heads");
+    return G4_OK;
+}
+
+int g4_attend_decode(g4_ctx *ctx, const float *q, const float *k_cache, const float *v_cache,
+                     int64_t row_stride, int64_t kv_begin, int64_t kv_end, int n_heads,
+                     int n_kv_heads, int head_dim, float scale, float *out, g4_stream stream) {
+    return guarded([&] {
+        g4::clear_error();
+        if (!ctx) return invalid("g4_attend_decode: null context");
+        int rc = check_heads(n_heads, n_kv_heads, head_dim);
+        if (rc != G4_OK) return rc;
+        if (row_stride < (int64_t)n_kv_heads * head_dim) return invalid("row_stride below the row width");
+        if (kv_begin < 0 || kv_end <= kv_begin)
+            return g4::set_error(G4_ERR_COMPUTE, "softmax input is not finite");
+        g4::DecodeArgs a{};
+        a.B = 1;
+        a.q = q;
+        a.k = k_cache;
+        a.v = v_cache;
+        a.row_stride = row_stride;
+        a.kv_begin0 = kv_begin;
+        a.kv_end0 = kv_end;
+        a.max_kv_len = kv_end - kv_begin;
+        a.prefill_window = -1;
+        a.n_heads = n_heads;
+        a.n_kv_heads = n_kv_heads;
+        a.head_dim = head_dim;
+        a.scale = scale;
+        a.out = out;
+        return g4::launch_decode(ctx, a, as_stream(stream));
+    });
+}
+
+int g4_attend_decode_batch(g4_ctx *ctx, int B, const float *q, const float *k_base,
+                           const float *v_base, int64_t row_stride, const int64_t *seq_row0,
+                           const int64_t *kv_begin, const int64_t *kv_end, int64_t max_kv_len,
+                           int n_heads, int n_kv_heads, int head_dim, float scale, float *out,
+                           g4_stream stream) {
+    return guarded([&] {
+        g4::clear_error();
+        if (!ctx) return invalid("g4_attend_decode_batch: null context");
+        if (B < 0) return invalid("negative batch size");
+        if (B == 0) return (int)G4_OK;
+        int rc = check_heads(n_heads, n_kv_heads, head_dim);
+        if (rc != G4_OK) return rc;
+        if (!kv_begin || !kv_end) return invalid("kv_begin and kv_end are required");
+        if (max_kv_len <= 0) return invalid("max_kv_len must be positive");
+        if (row_stride < (int64_t)n_kv_heads * head_dim) return invalid("row_stride below the row width");
+        g4::DecodeArgs a{};
+        a.B = B;
+        a.q = q;
+        a.k = k_base;
+        a.v = v_base;
+        a.row_stride = row_stride;
+        a.seq_row0 = seq_row0;
+        a.kv_begin = kv_begin;
+        a.kv_end = kv_end;
+        a.max_kv_len = max_kv_len;
+        a.prefill_window = -1;
+        a.n_heads = n_heads;
+        a.n_kv_heads = n_kv_heads;
+        a.head_dim = head_dim;
+        a.scale = scale;
+        a.out = out;
+        return g4::launch_decode(ctx, a, as_stream(stream));
+    });
+}
+
+int g4_attend_prefill(g4_ctx *ctx, const float *q, const float *k_cache, const float *v_cache,
+                      int64_t row_stride, int64_t pos0, int64_t N, int64_t window, int n_heads,
+                      int n_kv_heads, int head_dim, float scale, float *out, g4_stream stream) {
+    return guarded([&] {
+        g4::clear_error();
+        if (!ctx) return invalid("g4_attend_prefill: null context");
+        if (N < 0 || pos0 < 0 || window < 0) return invalid("prefill needs N, pos0, window >= 0");
+        if (N == 0) return (int)G4_OK;
+        int rc = check_heads(n_heads, n_kv_heads, head_dim);
+        if (rc != G4_OK) return rc;
+        if (row_stride < (int64_t)n_kv_heads * head_dim) return invalid("row_stride below the row width");
+        g4::PrefillArgs a{};
+        a.q = q;
+        a.k = k_cache;
+        a.v = v_cache;
+        a.row_stride = row_stride;
+        a.pos0 = pos0;
+        a.N = N;
+        a.window = window;
+        a.n_heads = n_heads;
+        a.n_kv_heads = n_kv_heads;
+        a.head_dim = head_dim;
+        a.scale = scale;
+        a.out = out;
+        return g4::launch_prefill(ctx, a, as_stream(stream));
+    });
+}
+
+int g4_attend(g4_ctx *ctx, const float *q_host, size_t q_len, const float *keys_host,
+              const float *values_host, size_t T, size_t n_heads, size_t n_kv_heads, float scale,
+              float *out_host) {
+    return guarded([&] {
+        g4::clear_error();
+        if (!ctx) return invalid("g4_attend: null context");
+        if (n_heads == 0 || n_kv_heads == 0) return invalid("attention needs positive head counts");
+        const size_t head_dim = q_len / n_heads;
+        if (head_dim == 0) return invalid("q is shorter than n_heads");
+        // model.rs:362-364: an empty context fails the softmax of every head.
+        if (T == 0) return g4::set_error(G4_ERR_COMPUTE, "softmax input is not finite");
+        const size_t width = n_kv_heads * head_dim;
+        const size_t used_q = n_heads * head_dim;
+        G4_HIP(hipSetDevice(ctx->device));
+        float *dq = nullptr, *dk = nullptr, *dv = nullptr, *dout = nullptr;
+        auto release = [&] {
+            if (dq) (void)hipFree(dq);
+            if (dk) (void)hipFree(dk);
+            if (dv) (void)hipFree(dv);
+            if (dout) (void)hipFree(dout);
+        };
+        hipError_t e = hipMalloc(&dq, used_q * sizeof(float));
+        if (e == hipSuccess) e = hipMalloc(&dk, T * width * sizeof(float));
+        if (e == hipSuccess) e = hipMalloc(&dv, T * width * sizeof(float));
+        if (e == hipSuccess) e = hipMalloc(&dout, used_q * sizeof(float));
+        if (e == hipSuccess) e = hipMemcpy(dq, q_host, used_q * sizeof(float), hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemcpy(dk, keys_host, T * width * sizeof(float), hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemcpy(dv, values_host, T * width * sizeof(float), hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            release();
+            return g4::hip_failed(e, "g4_attend staging");
+        }
+        int rc = g4_attend_decode(ctx, dq, dk, dv, (int64_t)width, 0, (int64_t)T, (int)n_heads,
+                                  (int)n_kv_heads, (int)head_dim, scale, dout, nullptr);
+        if (rc == G4_OK) rc = g4_check_status(ctx, nullptr);
+        if (rc == G4_OK) {
+            e = hipMemcpy(out_host, dout, used_q * sizeof(float), hipMemcpyDeviceToHost);
+            if (e != hipSuccess) rc = g4::hip_failed(e, "g4_attend result");
+        }
+        release();
+        return rc;
+    });
+}
+
+// ---------------------------------------------------------------- preparation
+int g4_rms_norm_rows(g4_ctx *ctx, const float *x, int64_t n_rows, int64_t width,
+                     const float *weight, float eps, float *out, g4_stream stream) {
+    return guarded([&] {
+        g4::clear_error();
+        if (!ctx) return invalid("g4_rms_norm_rows: null context");
+        if (width <= 0 || eps < 0.0f || n_rows < 0)
+            return g4::set_error(G4_ERR_COMPUTE, "invalid RMS norm inputs");
+        return g4::launch_rms_norm_rows(x, n_rows, width, weight, eps, out, as_stream(stream));
+    });
+}
+
+int g4_rope_neox_rows(g4_ctx *ctx, float *x, int64_t n_tokens, int n_heads, int head_dim,
+                      int n_rot, int64_t pos0, float base, const float *freq_factors,
+                      int64_t n_factors, g4_stream stream) {
+    return guarded([&] {
+        g4::clear_error();
+        if (!ctx) return invalid("g4_rope_neox_rows: null context");
+        const int half = n_rot / 2;
+        // ops.rs:142-149
+        if (n_rot <= 0 || n_rot % 2 != 0 || n_rot > head_dim || base <= 0.0f ||
+            (freq_factors && n_factors < half) || n_heads <= 0 || n_tokens < 0 || pos0 < 0)
+            return g4::set_error(G4_ERR_COMPUTE, "invalid RoPE inputs");
+        // The reference computes base.powf(-2.0 / n_rot) on the host's libm.
+        const float theta_scale = powf(base, -2.0f / (float)n_rot);
+        return g4::launch_rope_rows(x, n_tokens, n_heads, head_dim, n_rot, pos0, theta_scale,
+                                    freq_factors, as_stream(stream));
+    });
+}
+
+// ------------------------------------------------------------------ KvCache
+int g4_kv_create(g4_ctx *ctx, int n_layers, const int64_t *widths, int64_t capacity,
+                 g4_kv_cache **out) {
+    return guarded([&] {
+        g4::clear_error();
+        if (!ctx || !out || !widths) return invalid("g4_kv_create: null argument");
+        if (n_layers <= 0 || capacity <= 0) return invalid("g4_kv_create: empty cache shape");
+        *out = nullptr;
+        G4_HIP(hipSetDevice(ctx->device));
+        auto *c = new g4_kv_cache();
+        c->ctx = ctx;
+        c->n_layers = n_layers;
+        c->capacity = capacity;
+        c->width.assign(widths, widths + n_layers);
+        c->k.assign(n_layers, nullptr);
+        c->v.assign(n_layers, nullptr);
+        c->rows.assign(n_layers, 0);
+        for (int l = 0; l < n_layers; ++l) {
+            if (c->width[l] <= 0) continue;
+            const size_t bytes = (size_t)capacity * c->width[l] * sizeof(float);
+            hipError_t e = hipMalloc(&c->k[l], bytes);
+            if (e == hipSuccess) e = hipMalloc(&c->v[l], bytes);
+            if (e != hipSuccess) {
+                g4_kv_destroy(c);
+                return g4::hip_failed(e, "g4_kv_create");
+            }
+        }
+        *out = c;
+        return (int)G4_OK;
+    });
+}
+
+int g4_kv_destroy(g4_kv_cache *c) {
+    if (!c) return G4_OK;
+    (void)hipDeviceSynchronize();
+    for (size_t l = 0; l < c->k.size(); ++l) {
+        if (c->k[l]) (void)hipFree(c->k[l]);
+        if (c->v[l]) (void)hipFree(c->v[l]);
+    }
+    delete c;
+    return G4_OK;
+}
+
+int g4_kv_append_rows(g4_kv_cache *c, int layer, const float *k, const float *v, int64_t n,
+                      g4_stream stream) {
+    return guarded([&] {
+        g4::clear_error();
+        if (!c) return invalid("g4_kv_append: null cache");
+        if (layer < 0 || layer >= c->n_layers) return invalid("g4_kv_append: layer outside the cache");
+        if (n < 0) return invalid("g4_kv_append: negative row count");
+        if (c->width[layer] <= 0) return invalid("g4_kv_append: layer keeps no K/V");
+        if (c->rows[layer] + n > c->capacity)
+            return g4::set_error(G4_ERR_CONTEXT_TOO_LONG,
+                                 "context length " + std::to_string(c->rows[layer] + n) +
+                                     " exceeds configured max " + std::to_string(c->capacity),
+                                 (uint64_t)(c->rows[layer] + n), (uint64_t)c->capacity);
+        const size_t row_bytes = (size_t)c->width[layer] * sizeof(float);
+        const size_t off = (size_t)c->rows[layer] * c->width[layer];
+        G4_HIP(hipMemcpyAsync(c->k[layer] + off, k, row_bytes * n, hipMemcpyDeviceToDevice, as_stream(stream)));
+        G4_HIP(hipMemcpyAsync(c->v[layer] + off, v, row_bytes * n, hipMemcpyDeviceToDevice, as_stream(stream)));
+        c->rows[layer] += n;
+        // context_memory.rs:44-47: appending to layer L makes layers 0..=L exist.
+        if (layer + 1 > c->known_layers) c->known_layers = layer + 1;
+        return (int)G4_OK;
+    });
+}
+
+int g4_kv_append(g4_kv_cache *c, int layer, const float *k, const float *v, g4_stream stream) {
+    return g4_kv_append_rows(c, layer, k, v, 1, stream);
+}
+
+int g4_kv_view(const g4_kv_cache *c, int layer, int64_t len, const float **k, const float **v,
+               int64_t *row_stride) {
+    g4::clear_error();
+    if (!c || !k || !v) return invalid("g4_kv_view: null argument");
+    if (layer < 0 || len < 0) return invalid("g4_kv_view: negative layer or length");
+    // context_memory.rs:53-69
+    if (layer >= c->known_layers) {
+        if (len == 0) {
+            *k = *v = nullptr;
+            if (row_stride) *row_stride = 0;
+            return G4_OK;
+        }
+        return g4::set_error(G4_ERR_MISSING_LAYER, "layer " + std::to_string(layer) + " has no cached K/V",
+                             (uint64_t)layer);
+    }
+    const int64_t have = layer < c->n_layers ? c->rows[layer] : 0;
+    if (len > have)
+        return g4::set_error(G4_ERR_CONTEXT_TOO_LONG,
+                             "context length " + std::to_string(len) + " exceeds configured max " +
+                                 std::to_string(have),
+                             (uint64_t)len, (uint64_t)have);
+    *k = c->k[layer];
+    *v = c->v[layer];
+    if (row_stride) *row_stride = c->width[layer];
+    return G4_OK;
+}
+
+int64_t g4_kv_len(const g4_kv_cache *c, int layer) {
+    if (!c || layer < 0 || layer >= c->n_layers) return 0;
+    return c->rows[layer];
+}
+
+void g4_kv_clear(g4_kv_cache *c) {
+    if (!c) return;
+    for (auto &r : c->rows) r = 0;
+    c->known_layers = 0;
+}
+
+// ------------------------------------------------------------------ policies
+int g4_layer_is_global(int n_layers, int layer) {
+    return (layer + 1 == n_layers || layer % 5 == 4) ? 1 : 0;
+}
+
+int g4_kv_source_layer(int n_layers, int shared_kv_layers, int layer, int *source) {
+    g4::clear_error();
+    if (!source) return invalid("g4_kv_source_layer: null output");
+    if (layer < 0 || layer >= n_layers)
+        return g4::set_error(G4_ERR_COMPUTE, "layer " + std::to_string(layer) +
+                                                 " must be within n_layers " + std::to_string(n_layers));
+    if (shared_kv_layers < 0 || shared_kv_layers >= n_layers)
+        return g4::set_error(G4_ERR_COMPUTE, std::to_string(shared_kv_layers) +
+                                                 " KV-shared layers leave no layer of " +
+                                                 std::to_string(n_layers) + " to own a cache");
+    const int first_shared = n_layers - shared_kv_layers;
+    if (layer < first_shared) {
+        *source = layer;
+        return G4_OK;
+    }
+    const int kind = g4_layer_is_global(n_layers, layer);
+    for (int e = first_shared - 1; e >= 0; --e) {
+        if (g4_layer_is_global(n_layers, e) == kind) {
+            *source = e;
+            return G4_OK;
+        }
+    }
+    return g4::set_error(G4_ERR_COMPUTE, "KV-shared layer " + std::to_string(layer) +
+                                             " has no earlier layer of the same attention kind");
+}
+
+void g4_windowed_len(int64_t seq_len, int64_t window, int64_t *begin, int64_t *end) {
+    if (begin) *begin = seq_len > window ? seq_len - window : 0;
+    if (end) *end = seq_len;
+}
+
+void g4_proportional_rope_freq_factors(int head_dim, float p, float *out) {
+    if (!out || head_dim <= 0) return;
+    const float r = (float)head_dim * p / 2.0f;
+    const int64_t rotated = r > 0.0f ? (int64_t)r : 0;
+    for (int pair = 0; pair < head_dim / 2; ++pair) out[pair] = pair < rotated ? 1.0f : 1e30f;
+}
+
+// --------------------------------------------------------- layer attention
+int g4_layer_attention(g4_ctx *ctx, g4_kv_cache *cache, const g4_hparams *hp, int layer,
+                       int64_t position, float *q, float *k, float *v, const float *q_norm_w,
+                       const float *k_norm_w, const float *rope_freqs, float *out, int *source_out,
+                       int64_t *begin_out, int64_t *end_out, g4_stream stream) {
+    return guarded([&] {
+        g4::clear_error();
+        if (!ctx || !cache || !hp) return invalid("g4_layer_attention: null argument");
+        if (layer < 0 || layer >= hp->n_layers) return invalid("g4_layer_attention: layer outside n_layers");
+        if (position < 0) return invalid("g4_layer_attention: negative position");
+        const bool global = g4_layer_is_global(hp->n_layers, layer) != 0;
+        const int head_dim = global ? hp->head_dim_global : hp->head_dim_local;
+        const float base = global ? hp->global_rope_base : hp->local_rope_base;
+        const float *factors = global ? rope_freqs : nullptr;
+        const int64_t n_factors = factors ? head_dim / 2 : 0;
+        const hipStream_t st = as_stream(stream);
+        // model.rs:395-396
+        int rc = g4_rms_norm_rows(ctx, q, hp->n_heads, head_dim, q_norm_w, hp->rms_norm_eps, q, stream);
+        if (rc == G4_OK)
+            rc = g4_rope_neox_rows(ctx, q, 1, hp->n_heads, head_dim, head_dim, position, base, factors,
+                                   n_factors, stream);
+        if (rc != G4_OK) return rc;
+        // model.rs:398
+        int source = 0;
+        rc = g4_kv_source_layer(hp->n_layers, hp->shared_kv_layers, layer, &source);
+        if (rc != G4_OK) return rc;
+        if (source == layer) {  // model.rs:399-406
+            rc = g4_rms_norm_rows(ctx, k, hp->n_kv_heads, head_dim, k_norm_w, hp->rms_norm_eps, k, stream);
+            if (rc == G4_OK)
+                rc = g4_rms_norm_rows(ctx, v, hp->n_kv_heads, head_dim, nullptr, hp->rms_norm_eps, v, stream);
+            if (rc == G4_OK)
+                rc = g4_rope_neox_rows(ctx, k, 1, hp->n_kv_heads, head_dim, head_dim, position, base,
+                                       factors, n_factors, stream);
+            if (rc == G4_OK) rc = g4_kv_append(cache, layer, k, v, stream);
+            if (rc != G4_OK) return rc;
+        }
+        // model.rs:407-408
+        const float *keys = nullptr, *values = nullptr;
+        int64_t stride = 0;
+        rc = g4_kv_view(cache, source, position + 1, &keys, &values, &stride);
+        if (rc != G4_OK) return rc;
+        int64_t begin = 0, end = position + 1;
+        if (!global) g4_windowed_len(position + 1, hp->sliding_window, &begin, &end);
+        if (stride != (int64_t)hp->n_kv_heads * head_dim)
+            return invalid("g4_layer_attention: source layer's row width differs from this layer's");
+        if (source_out) *source_out = source;
+        if (begin_out) *begin_out = begin;
+        if (end_out) *end_out = end;
+        (void)st;
+        // model.rs:409-410: q and k are RMS-normalised, so the scale is 1.0.
+        return g4_attend_decode(ctx, q, keys, values, stride, begin, end, hp->n_heads,
+                                hp->n_kv_heads, head_dim, 1.0f, out, stream);
+    });
+}
+
+// ------------------------------------------------------------- ComputePort
+int g4_port_matmul(g4_ctx *ctx, const float *a, const float *b, int64_t m, int64_t n, int64_t k,
+                   float *out, g4_stream stream) {
+    return guarded([&] {
+        g4::clear_error();
+        if (!ctx) return invalid("g4_port_matmul: null context");
+        if (m < 0 || n < 0 || k < 0) return g4::set_error(G4_ERR_COMPUTE, "matmul dimensions overflow");
+        return g4::launch_matmul(a, b, m, n, k, out, as_stream(stream));
+    });
+}
+
+int g4_port_rms_norm(g4_ctx *ctx, const float *x, const float *weight, int64_t n, float eps,
+                     float *out, g4_stream stream) {
+    return g4_rms_norm_rows(ctx, x, 1, n, weight, eps, out, stream);
+}
+
+int g4_port_softmax(g4_ctx *ctx, const float *x, int64_t n, float *out, g4_stream stream) {
+    return guarded([&] {
+        g4::clear_error();
+        if (!ctx) return invalid("g4_port_softmax: null context");
+        if (n <= 0) return g4::set_error(G4_ERR_COMPUTE, "softmax requires a non-empty buffer");
+        int rc = g4::launch_softmax(x, n, out, ctx->status_dev, as_stream(stream));
+        if (rc != G4_OK) return rc;
+        // ComputePort::softmax returns its error directly, so this call waits.
+        return g4_check_status(ctx, stream);
+    });
+}
+
+int g4_port_rope(g4_ctx *ctx, float *x, int64_t len, int64_t pos, float theta, int64_t dims,
+                 g4_stream stream) {
+    return guarded([&] {
+        g4::clear_error();
+        if (!ctx) return invalid("g4_port_rope: null context");
+        if (dims <= 0 || dims % 2 != 0 || dims > len || theta <= 0.0f || pos < 0)
+            return g4::set_error(G4_ERR_COMPUTE, "invalid RoPE inputs");
+        return g4_rope_neox_rows(ctx, x, 1, 1, (int)len, (int)dims, pos, theta, nullptr, 0, stream);
+    });
+}
+
+int g4_port_add(g4_ctx *ctx, const float *a, const float *b, int64_t n, float *out,
+                g4_stream stream) {
+    return guarded([&] {
+        g4::clear_error();
+        if (!ctx) return invalid("g4_port_add: null context");
+        if (n < 0) return g4::set_error(G4_ERR_COMPUTE, "add buffer lengths differ");
+        return g4::launch_add(a, b, n, out, as_stream(stream));
+    });
+}
+
+}  // extern "C"

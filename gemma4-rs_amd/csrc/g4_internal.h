@@ -1,0 +1,97 @@
+// Internal declarations shared by the backend's translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/g4attn.h"
+
+namespace g4 {
+
+// Error state of the calling thread, read back through g4_last_error().
+int set_error(int code, const std::string &message, uint64_t a = 0, uint64_t b = 0);
+void clear_error();
+
+// hipError_t -> EngError::Compute("hip: ...").
+int hip_failed(hipError_t e, const char *what);
+
+#define G4_HIP(call)                                                   \
+    do {                                                               \
+        hipError_t e_ = (call);                                        \
+        if (e_ != hipSuccess) return ::g4::hip_failed(e_, #call);      \
+    } while (0)
+
+// Status bits the kernels raise in the context's device status word.
+enum : unsigned {
+    kStatusNonFinite = 1u,   // softmax input not finite (model.rs:362-364)
+    kStatusRangeTooLong = 2u // a ragged range exceeded max_kv_len
+};
+
+struct Workspace {
+    void *ptr = nullptr;
+    size_t bytes = 0;
+};
+
+}  // namespace g4
+
+struct g4_ctx {
+    int device = 0;
+    unsigned *status_dev = nullptr;  // kStatus* bits, cleared by g4_check_status
+    g4::Workspace ws;                // split-K partials of the decode kernels
+    int64_t decode_chunk = 0;        // 0 = automatic
+    int num_cus = 256;
+};
+
+namespace g4 {
+
+// Grows the context's workspace to at least `bytes` (stream-ordered users
+// must not be in flight on another stream when it grows).
+int ensure_workspace(g4_ctx *ctx, size_t bytes, hipStream_t stream);
+
+// Launchers implemented in the .hip files.
+struct DecodeArgs {
+    int B;
+    const float *q;
+    const float *k;
+    const float *v;
+    int64_t row_stride;
+    const int64_t *seq_row0;  // device or null
+    const int64_t *kv_begin;  // device or null -> kv_begin0 for every sequence
+    const int64_t *kv_end;    // device or null -> kv_end0
+    int64_t kv_begin0, kv_end0;
+    int64_t max_kv_len;
+    // Prefill form: when `prefill_window >= 0`, sequence s is query s at
+    // position pos0 + s, with range [(p+1-window)+ or 0, p+1).
+    int64_t pos0;
+    int64_t prefill_window;  // -1: not prefill; 0: global; >0: sliding window
+    int n_heads, n_kv_heads, head_dim;
+    float scale;
+    float *out;
+};
+int launch_decode(g4_ctx *ctx, const DecodeArgs &a, hipStream_t stream);
+
+struct PrefillArgs {
+    const float *q;
+    const float *k;
+    const float *v;
+    int64_t row_stride;
+    int64_t pos0, N, window;
+    int n_heads, n_kv_heads, head_dim;
+    float scale;
+    float *out;
+};
+int launch_prefill(g4_ctx *ctx, const PrefillArgs &a, hipStream_t stream);
+
+int launch_rms_norm_rows(const float *x, int64_t n_rows, int64_t width, const float *w, float eps,
+                         float *out, hipStream_t stream);
+int launch_rope_rows(float *x, int64_t n_tokens, int n_heads, int head_dim, int n_rot,
+                     int64_t pos0, float theta_scale, const float *factors, hipStream_t stream);
+int launch_matmul(const float *a, const float *b, int64_t m, int64_t n, int64_t k, float *out,
+                  hipStream_t stream);
+int launch_softmax(const float *x, int64_t n, float *out, unsigned *status, hipStream_t stream);
+int launch_add(const float *a, const float *b, int64_t n, float *out, hipStream_t stream);
+
+}  // namespace g4

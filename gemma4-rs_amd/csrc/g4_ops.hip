@@ -1,0 +1,181 @@
+// Attention input preparation (per-head RMS norm, NEOX RoPE) and the
+// ComputePort method set on the device.  Citations: crates/llm-backend-cpu/src/ops.rs.
+
+#include "g4_internal.h"
+
+namespace g4 {
+namespace {
+
+// rms_norm (ops.rs:45-56) on rows of `width` floats, one wavefront per row.
+// The mean of squares is accumulated in f64 from f32-rounded squares, as the
+// reference does; the f64 tree sum differs from the sequential one only in
+// bits far below the f32 rounding of the mean.
+__global__ __launch_bounds__(256) void rms_norm_rows_kernel(const float *x, int64_t n_rows,
+                                                            int64_t width, const float *w,
+                                                            float eps, float *out) {
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= n_rows) return;
+    const float *xr = x + row * width;
+    double sum = 0.0;
+    for (int64_t i = lane; i < width; i += 64) {
+        const float v = xr[i];
+        const float sq = v * v;
+        sum += (double)sq;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+    const float mean = (float)(sum / (double)width);
+    // 1 / sqrt(mean + eps) with the f32 rounding of each step: sqrt and the
+    // division are done in f64 and rounded once to f32, which for these two
+    // operations equals the correctly rounded f32 result (53 >= 2*24 + 2).
+    const float root = (float)sqrt((double)(mean + eps));
+    const float scale = (float)(1.0 / (double)root);
+    float *orow = out + row * width;
+    for (int64_t i = lane; i < width; i += 64) {
+        const float v = xr[i] * scale;
+        orow[i] = w ? v * w[i] : v;
+    }
+}
+
+// rope_neox (ops.rs:134-162) on every head of one token per workgroup.  The
+// angle of pair i is theta_i / factor_i with theta_0 = position and
+// theta_{i+1} = theta_i * theta_scale in f32 -- a sequential recurrence, so
+// one lane builds the table and the workgroup applies it.
+__global__ __launch_bounds__(256) void rope_rows_kernel(float *x, int n_heads, int head_dim,
+                                                        int n_rot, int64_t pos0,
+                                                        float theta_scale,
+                                                        const float *factors) {
+#pragma clang fp contract(off)
+    extern __shared__ float theta[];  // [n_rot/2]
+    const int half = n_rot / 2;
+    const int64_t token = blockIdx.x;
+    if (threadIdx.x == 0) {
+        float t = (float)(pos0 + token);
+        for (int i = 0; i < half; ++i) {
+            theta[i] = t;
+            t = t * theta_scale;
+        }
+    }
+    __syncthreads();
+    float *xt = x + token * (int64_t)n_heads * head_dim;
+    for (int e = threadIdx.x; e < n_heads * half; e += blockDim.x) {
+        const int h = e / half, i = e % half;
+        const float factor = factors ? factors[i] : 1.0f;
+        const float angle = theta[i] / factor;
+        float sn, cs;
+        sincosf(angle, &sn, &cs);
+        float *xh = xt + (int64_t)h * head_dim;
+        const float a = xh[i], b = xh[i + half];
+        xh[i] = a * cs - b * sn;
+        xh[i + half] = a * sn + b * cs;
+    }
+}
+
+// matmul_f32 (ops.rs:9-39): row-major [m,k] x [k,n], sequential inner sum of
+// rounded products, as the reference's triple loop.
+__global__ void matmul_kernel(const float *a, const float *b, int64_t m, int64_t n, int64_t k,
+                              float *out) {
+#pragma clang fp contract(off)
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= m * n) return;
+    const int64_t row = idx / n, col = idx % n;
+    float acc = 0.0f;
+    for (int64_t i = 0; i < k; ++i) acc += a[row * k + i] * b[i * n + col];
+    out[idx] = acc;
+}
+
+// Total order of f32::total_cmp as a signed key.
+__device__ inline int total_key(float x) {
+    int bits = __float_as_int(x);
+    return bits ^ (int)(((unsigned)(bits >> 31)) >> 1);
+}
+
+// softmax_f32 (ops.rs:105-127) of one vector in one workgroup.
+__global__ __launch_bounds__(256) void softmax_kernel(const float *x, int64_t n, float *out,
+                                                      unsigned *status) {
+    __shared__ int kmax[256];
+    __shared__ float red[256];
+    const int tid = threadIdx.x;
+    int best = INT_MIN;
+    for (int64_t i = tid; i < n; i += 256) best = max(best, total_key(x[i]));
+    kmax[tid] = best;
+    __syncthreads();
+    for (int off = 128; off > 0; off >>= 1) {
+        if (tid < off) kmax[tid] = max(kmax[tid], kmax[tid + off]);
+        __syncthreads();
+    }
+    const int kb = kmax[0];
+    const float mx = __int_as_float(kb ^ (int)(((unsigned)(kb >> 31)) >> 1));
+    float s = 0.0f;
+    for (int64_t i = tid; i < n; i += 256) {
+        const float e = expf(x[i] - mx);
+        out[i] = e;
+        s += e;
+    }
+    red[tid] = s;
+    __syncthreads();
+    for (int off = 128; off > 0; off >>= 1) {
+        if (tid < off) red[tid] = red[tid] + red[tid + off];
+        __syncthreads();
+    }
+    const float sum = red[0];
+    if (!isfinite(sum) || sum == 0.0f) {
+        if (tid == 0) atomicOr(status, kStatusNonFinite);
+        return;
+    }
+    for (int64_t i = tid; i < n; i += 256) out[i] = out[i] / sum;
+}
+
+__global__ void add_kernel(const float *a, const float *b, int64_t n, float *out) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = a[i] + b[i];
+}
+
+}  // namespace
+
+int launch_rms_norm_rows(const float *x, int64_t n_rows, int64_t width, const float *w, float eps,
+                         float *out, hipStream_t stream) {
+    if (n_rows <= 0) return G4_OK;
+    hipLaunchKernelGGL(rms_norm_rows_kernel, dim3((unsigned)((n_rows + 3) / 4)), dim3(256), 0,
+                       stream, x, n_rows, width, w, eps, out);
+    G4_HIP(hipGetLastError());
+    return G4_OK;
+}
+
+int launch_rope_rows(float *x, int64_t n_tokens, int n_heads, int head_dim, int n_rot,
+                     int64_t pos0, float theta_scale, const float *factors, hipStream_t stream) {
+    if (n_tokens <= 0) return G4_OK;
+    hipLaunchKernelGGL(rope_rows_kernel, dim3((unsigned)n_tokens), dim3(256),
+                       (size_t)(n_rot / 2) * sizeof(float), stream, x, n_heads, head_dim, n_rot,
+                       pos0, theta_scale, factors);
+    G4_HIP(hipGetLastError());
+    return G4_OK;
+}
+
+int launch_matmul(const float *a, const float *b, int64_t m, int64_t n, int64_t k, float *out,
+                  hipStream_t stream) {
+    const int64_t total = m * n;
+    if (total <= 0) return G4_OK;
+    hipLaunchKernelGGL(matmul_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream,
+                       a, b, m, n, k, out);
+    G4_HIP(hipGetLastError());
+    return G4_OK;
+}
+
+int launch_softmax(const float *x, int64_t n, float *out, unsigned *status, hipStream_t stream) {
+    hipLaunchKernelGGL(softmax_kernel, dim3(1), dim3(256), 0, stream, x, n, out, status);
+    G4_HIP(hipGetLastError());
+    return G4_OK;
+}
+
+int launch_add(const float *a, const float *b, int64_t n, float *out, hipStream_t stream) {
+    if (n <= 0) return G4_OK;
+    hipLaunchKernelGGL(add_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, a, b,
+                       n, out);
+    G4_HIP(hipGetLastError());
+    return G4_OK;
+}
+
+}  // namespace g4

@@ -1,0 +1,198 @@
+/*
+ * g4attn.h -- C ABI of the MI355X (gfx950) attention backend for gemma4-rs.
+ *
+ * The backend replaces the engine's CPU attention seam: the private
+ * `attend(q, keys, values, n_heads, n_kv_heads, scale)` that
+ * Gemma4CpuModel::layer calls once per layer
+ * (crates/llm-gemma4/src/impl_/model.rs:348-366, call site model.rs:410),
+ * together with the primitives it is assembled from and the engine ports it
+ * reads (ComputePort, ContextMemory, EngError).  Citations are file:line in
+ * the gemma4-rs repository.
+ *
+ * Conventions
+ *  - Every function returns a g4_status; 0 is success.  On failure
+ *    g4_last_error() holds the message with the reference's wording and
+ *    g4_last_error_fields() the numbers of ContextTooLong / MissingLayer.
+ *    Nothing panics or aborts across the ABI.
+ *  - "_dev" pointers are device (HBM) pointers owned by the caller; host
+ *    pointers are marked "host".  No function keeps a pointer after it
+ *    returns, except the KV-cache object, which owns its device rows.
+ *  - stream is a hipStream_t (NULL = the null stream).  Device-pointer entry
+ *    points are asynchronous and stream-ordered; their softmax failures are
+ *    recorded on the device and reported by g4_check_status().  Host-pointer
+ *    entry points synchronise and report failures directly.
+ *  - A K/V cache is rows of n_kv_heads*head_dim f32, row t = position t,
+ *    oldest first, as the reference's KvCache keeps them
+ *    (crates/llm-eng/src/context_memory.rs:44-51, model.rs:312-321);
+ *    `row_stride` is the distance between rows in floats.
+ */
+#ifndef G4ATTN_H
+#define G4ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* EngError variants (crates/llm-eng/src/error.rs:3-15). */
+typedef enum {
+    G4_OK = 0,
+    G4_ERR_CONTEXT_TOO_LONG = 1, /* EngError::ContextTooLong { got, max } */
+    G4_ERR_MISSING_LAYER = 2,    /* EngError::MissingLayer(layer) */
+    G4_ERR_MISSING_WEIGHT = 3,   /* EngError::MissingWeight(name) */
+    G4_ERR_COMPUTE = 4,          /* EngError::Compute(message) */
+    G4_ERR_MSG = 5               /* EngError::Msg(message) */
+} g4_status;
+
+typedef struct g4_ctx g4_ctx;           /* one per device */
+typedef struct g4_kv_cache g4_kv_cache; /* device-resident ContextMemory */
+typedef void *g4_stream;                /* hipStream_t */
+
+/* Message of the last failure on the calling thread ("" if none). */
+const char *g4_last_error(void);
+/* ContextTooLong: *a = got, *b = max.  MissingLayer: *a = layer. */
+void g4_last_error_fields(uint64_t *a, uint64_t *b);
+
+/* ---------------------------------------------------------------- context */
+int g4_init(int device, g4_ctx **ctx);
+int g4_release(g4_ctx *ctx);
+/* Waits for `stream`, then reports (and clears) any softmax failure the
+ * device-pointer attention calls recorded since the last check, as
+ * G4_ERR_COMPUTE "softmax input is not finite" (model.rs:362-364). */
+int g4_check_status(g4_ctx *ctx, g4_stream stream);
+/* Tuning: keys per split-K work item of the decode kernels (0 = automatic). */
+int g4_set_decode_chunk(g4_ctx *ctx, int64_t keys);
+
+/* ------------------------------------------------------ attention (hot path) */
+/* attend (model.rs:348-366), host buffers: q[n_heads*head_dim] with
+ * head_dim = q_len / n_heads, keys/values [T][n_kv_heads*head_dim] (the
+ * `concat` image of model.rs:352-353), out[q_len].  Query head h reads KV head
+ * h*n_kv_heads/n_heads (model.rs:329).  Synchronous. */
+int g4_attend(g4_ctx *ctx, const float *q_host, size_t q_len, const float *keys_host,
+              const float *values_host, size_t T, size_t n_heads, size_t n_kv_heads, float scale,
+              float *out_host);
+
+/* One decode step over cache rows [kv_begin, kv_end) of k_cache/v_cache:
+ * the device form of `attend(q, &keys[range], &values[range], ...)` after
+ * `context.view(source, pos+1)` and the window range (model.rs:407-410). */
+int g4_attend_decode(g4_ctx *ctx, const float *q_dev, const float *k_cache_dev,
+                     const float *v_cache_dev, int64_t row_stride, int64_t kv_begin,
+                     int64_t kv_end, int n_heads, int n_kv_heads, int head_dim, float scale,
+                     float *out_dev, g4_stream stream);
+
+/* B independent decode steps in one launch (ragged lengths).  Sequence s
+ * reads rows [kv_begin[s], kv_end[s]) of its cache, whose row 0 is row
+ * seq_row0[s] of k_base/v_base (seq_row0 may be NULL: all zero).  The three
+ * arrays are device arrays of B int64; max_kv_len (host) must bound every
+ * kv_end[s]-kv_begin[s] (a longer range is reported as ContextTooLong by
+ * g4_check_status).  q and out are [B][n_heads*head_dim].  No reference
+ * counterpart: the engine is single-sequence (crates/llm-eng/src/schedule.rs:6-9);
+ * each sequence's result equals attend over its own rows. */
+int g4_attend_decode_batch(g4_ctx *ctx, int B, const float *q_dev, const float *k_base_dev,
+                           const float *v_base_dev, int64_t row_stride,
+                           const int64_t *seq_row0_dev, const int64_t *kv_begin_dev,
+                           const int64_t *kv_end_dev, int64_t max_kv_len, int n_heads,
+                           int n_kv_heads, int head_dim, float scale, float *out_dev,
+                           g4_stream stream);
+
+/* Chunked prefill: N queries at positions pos0..pos0+N-1, q and out
+ * [N][n_heads*head_dim].  Query i sees exactly the rows a decode at position
+ * p = pos0+i would: [0, p+1) when window == 0 (GlobalPolicy), else
+ * [(p+1-window)+, p+1) (LocalWindowPolicy, crates/llm-gemma4/src/eng/mod.rs:10-36),
+ * which is what the reference's token-at-a-time prompt loop computes
+ * (crates/llm-gemma4/src/impl_/generate.rs:37-41, model.rs:250).  The cache
+ * must hold rows up to pos0+N-1. */
+int g4_attend_prefill(g4_ctx *ctx, const float *q_dev, const float *k_cache_dev,
+                      const float *v_cache_dev, int64_t row_stride, int64_t pos0, int64_t N,
+                      int64_t window, int n_heads, int n_kv_heads, int head_dim, float scale,
+                      float *out_dev, g4_stream stream);
+
+/* ----------------------------------------- attention input preparation */
+/* rms_norm (crates/llm-backend-cpu/src/ops.rs:45-56) applied to each of
+ * n_rows rows of `width` floats (norm_heads, model.rs:283-290): f64 mean of
+ * squares, x * (1/sqrt(mean+eps)) * weight[i]; weight_dev may be NULL (V). */
+int g4_rms_norm_rows(g4_ctx *ctx, const float *x_dev, int64_t n_rows, int64_t width,
+                     const float *weight_dev, float eps, float *out_dev, g4_stream stream);
+
+/* rope_neox (ops.rs:134-162) in place on n_tokens x n_heads heads of
+ * head_dim floats (rope_heads, model.rs:295-304); token i sits at position
+ * pos0 + i.  Angles follow the reference's repeated f32 multiplication by
+ * base^(-2/n_rot); freq_factors_dev (n_rot/2 floats, may be NULL) divides
+ * them (global layers' rope_freqs). */
+int g4_rope_neox_rows(g4_ctx *ctx, float *x_dev, int64_t n_tokens, int n_heads, int head_dim,
+                      int n_rot, int64_t pos0, float base, const float *freq_factors_dev,
+                      int64_t n_factors, g4_stream stream);
+
+/* ------------------------------------- device-resident ContextMemory (KvCache) */
+/* context_memory.rs:11-86 with device rows: n_layers layers, layer l holding
+ * up to capacity rows of widths[l] floats (0 = layer keeps no cache). */
+int g4_kv_create(g4_ctx *ctx, int n_layers, const int64_t *widths_host, int64_t capacity,
+                 g4_kv_cache **cache);
+int g4_kv_destroy(g4_kv_cache *cache);
+/* append (context_memory.rs:44-51): copies one row of k and v (device). */
+int g4_kv_append(g4_kv_cache *cache, int layer, const float *k_dev, const float *v_dev,
+                 g4_stream stream);
+/* append of n consecutive rows (a prompt chunk's K/V). */
+int g4_kv_append_rows(g4_kv_cache *cache, int layer, const float *k_dev, const float *v_dev,
+                      int64_t n, g4_stream stream);
+/* view (context_memory.rs:53-69): the first len rows, or MissingLayer /
+ * ContextTooLong with the reference's numbers. */
+int g4_kv_view(const g4_kv_cache *cache, int layer, int64_t len, const float **k_dev,
+               const float **v_dev, int64_t *row_stride);
+int64_t g4_kv_len(const g4_kv_cache *cache, int layer);
+void g4_kv_clear(g4_kv_cache *cache); /* context_memory.rs:82-84 */
+
+/* --------------------------------------------------- layer attention driver */
+/* The Gemma4HyperParams fields attention reads (crates/llm-gemma4/src/idea/mod.rs:105-124). */
+typedef struct {
+    int n_layers, n_heads, n_kv_heads, head_dim_local, head_dim_global;
+    int64_t sliding_window;
+    int shared_kv_layers;
+    float local_rope_base, global_rope_base, rms_norm_eps;
+} g4_hparams;
+
+/* The attention segment of Gemma4CpuModel::layer (model.rs:386-411) from the
+ * projected q/k/v on, on the device: norm_heads(q, attn_q_norm), RoPE(q); for
+ * owner layers norm_heads(k, attn_k_norm), norm_heads(v, none), RoPE(k),
+ * append; view(kv_source_layer, pos+1); window range; attend(scale 1.0).
+ * q_dev [n_heads*head_dim] and k_dev/v_dev [n_kv_heads*head_dim] are
+ * normalised/rotated in place (k/v ignored on shared layers).  rope_freqs_dev
+ * ([head_dim_global/2]) is used on global layers.  source, kv_begin, kv_end
+ * (host, may be NULL) receive the attended set. */
+int g4_layer_attention(g4_ctx *ctx, g4_kv_cache *cache, const g4_hparams *hp, int layer,
+                       int64_t position, float *q_dev, float *k_dev, float *v_dev,
+                       const float *q_norm_w_dev, const float *k_norm_w_dev,
+                       const float *rope_freqs_dev, float *out_dev, int *source,
+                       int64_t *kv_begin, int64_t *kv_end, g4_stream stream);
+
+/* ----------------------------------------------------------- policies */
+/* layer_attention_kind (idea/mod.rs:238-246): 1 global, 0 local. */
+int g4_layer_is_global(int n_layers, int layer);
+/* kv_source_layer (crates/llm-gemma4/src/eng/mod.rs:71-90); KvShareError ->
+ * G4_ERR_COMPUTE with its Display text, as model.rs:398 maps it. */
+int g4_kv_source_layer(int n_layers, int shared_kv_layers, int layer, int *source);
+/* windowed_len (eng/mod.rs:10-12). */
+void g4_windowed_len(int64_t seq_len, int64_t window, int64_t *begin, int64_t *end);
+/* proportional_rope_freq_factors (idea/mod.rs:162-165), out[head_dim/2] host. */
+void g4_proportional_rope_freq_factors(int head_dim, float p, float *out_host);
+
+/* ------------------------------------- ComputePort (crates/llm-eng/src/compute.rs:3-29) */
+/* HipPort: the trait's method set on device buffers, with CpuPort's
+ * semantics (crates/llm-backend-cpu/src/port.rs:11-51). */
+int g4_port_matmul(g4_ctx *ctx, const float *a_dev, const float *b_dev, int64_t m, int64_t n,
+                   int64_t k, float *out_dev, g4_stream stream);           /* ops.rs:9-39 */
+int g4_port_rms_norm(g4_ctx *ctx, const float *x_dev, const float *weight_dev, int64_t n,
+                     float eps, float *out_dev, g4_stream stream);         /* ops.rs:58-60 */
+int g4_port_softmax(g4_ctx *ctx, const float *x_dev, int64_t n, float *out_dev,
+                    g4_stream stream);                                      /* ops.rs:105-127 */
+int g4_port_rope(g4_ctx *ctx, float *x_dev, int64_t len, int64_t pos, float theta,
+                 int64_t dims, g4_stream stream);                           /* ops.rs:164-166 */
+int g4_port_add(g4_ctx *ctx, const float *a_dev, const float *b_dev, int64_t n, float *out_dev,
+                g4_stream stream);                                          /* ops.rs:168-178 */
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* G4ATTN_H */

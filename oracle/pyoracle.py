@@ -1,0 +1,286 @@
+"""ctypes binding of the oracle (liboracle.so) -- TEST INFRASTRUCTURE ONLY.
+
+The oracle restates gemma4-rs's CPU attention path in C (g4_oracle.c).  It is
+the checker: only the test suite, the smoke check and the CPU-baseline leg of
+the benchmark load it.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+# G4_ORACLE_LIB selects a rebuilt variant (the planted-mistake test uses it).
+LIB_PATH = os.environ.get("G4_ORACLE_LIB") or os.path.join(HERE, "liboracle.so")
+
+OR_OK = 0
+OR_ERR_COMPUTE = 1
+OR_ERR_CONTEXT_TOO_LONG = 2
+OR_ERR_MISSING_LAYER = 3
+OR_ERR_KV_LAYER_OUT_OF_RANGE = 10
+OR_ERR_KV_TOO_MANY_SHARED = 11
+OR_ERR_KV_NO_EARLIER_SAME_KIND = 12
+
+_lib = None
+c_size = ctypes.c_size_t
+c_f32 = ctypes.c_float
+c_vp = ctypes.c_void_p
+P_f32 = ctypes.POINTER(ctypes.c_float)
+
+
+class OracleError(RuntimeError):
+    def __init__(self, code, message):
+        self.code = code
+        self.message = message
+        super().__init__(f"oracle status {code}: {message}")
+
+
+class Hparams(ctypes.Structure):
+    _fields_ = [
+        ("n_layers", c_size), ("n_heads", c_size), ("n_kv_heads", c_size), ("head_dim_local", c_size),
+        ("head_dim_global", c_size), ("sliding_window", c_size), ("shared_kv_layers", c_size),
+        ("local_rope_base", c_f32), ("global_rope_base", c_f32), ("rms_norm_eps", c_f32),
+    ]
+
+    @classmethod
+    def e2b(cls):
+        return cls(35, 8, 1, 256, 512, 512, 20, 10000.0, 1000000.0, 1e-6)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} missing: run `make -C oracle`")
+        L = ctypes.CDLL(LIB_PATH)
+        sig = {
+            "or_last_error": (ctypes.c_char_p, []),
+            "or_dot_f32": (c_f32, [c_vp, c_vp, c_size]),
+            "or_softmax_f32": (ctypes.c_int, [c_vp, c_size, c_vp]),
+            "or_rms_norm": (ctypes.c_int, [c_vp, c_size, c_vp, c_size, c_f32, c_vp]),
+            "or_rope_neox": (ctypes.c_int, [c_vp, c_size, c_size, c_f32, c_size, c_vp, c_size]),
+            "or_attend_head": (ctypes.c_int, [c_vp, c_vp, c_vp, c_size, c_size, c_size, c_size, c_size, c_f32,
+                                              c_size, c_vp]),
+            "or_attend": (ctypes.c_int, [c_vp, c_size, c_vp, c_vp, c_size, c_size, c_size, c_f32, c_vp]),
+            "or_attend_rows": (ctypes.c_int, [c_vp, c_size, c_vp, c_vp, c_size, c_size, c_size, c_f32, c_size,
+                                              c_vp]),
+            "or_attend_f64": (ctypes.c_int, [c_vp, c_size, c_vp, c_vp, c_size, c_size, c_size, ctypes.c_double,
+                                             c_vp]),
+            "or_norm_heads": (ctypes.c_int, [c_vp, c_size, c_size, c_vp, c_f32]),
+            "or_rope_heads": (ctypes.c_int, [c_vp, c_size, c_size, c_size, c_f32, c_vp, c_size]),
+            "or_layer_attention_kind": (ctypes.c_int, [c_size, c_size]),
+            "or_head_dim": (c_size, [c_size, c_size, c_size, c_size]),
+            "or_proportional_rope_freq_factors": (None, [c_size, c_f32, c_vp]),
+            "or_windowed_len": (None, [c_size, c_size, ctypes.POINTER(c_size), ctypes.POINTER(c_size)]),
+            "or_kv_source_layer": (ctypes.c_int, [c_size, c_size, c_size, ctypes.POINTER(c_size)]),
+            "or_kv_new": (c_vp, []),
+            "or_kv_free": (None, [c_vp]),
+            "or_kv_append": (ctypes.c_int, [c_vp, c_size, c_vp, c_vp, c_size]),
+            "or_kv_view": (ctypes.c_int, [c_vp, c_size, c_size, ctypes.POINTER(c_vp), ctypes.POINTER(c_vp),
+                                          ctypes.POINTER(c_size)]),
+            "or_kv_clear": (None, [c_vp]),
+            "or_layer_attention": (ctypes.c_int, [c_vp, ctypes.POINTER(Hparams), c_size, c_size, c_vp, c_vp, c_vp,
+                                                  c_vp, c_vp, c_vp, c_size, c_vp, ctypes.POINTER(c_size),
+                                                  ctypes.POINTER(c_size), ctypes.POINTER(c_size)]),
+            "or_pool_threads": (c_size, []),
+            "or_prepare_rows": (ctypes.c_int, [c_vp, c_size, c_size, c_size, c_vp, c_f32, c_size, c_f32, c_vp,
+                                               c_size]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _check(rc):
+    if rc != OR_OK:
+        raise OracleError(rc, lib().or_last_error().decode())
+
+
+def dot_f32(a, b):
+    a, b = _f32(a), _f32(b)
+    return lib().or_dot_f32(a.ctypes.data, b.ctypes.data, a.size)
+
+
+def softmax_f32(x):
+    x = _f32(x)
+    out = np.empty_like(x)
+    _check(lib().or_softmax_f32(x.ctypes.data, x.size, out.ctypes.data))
+    return out
+
+
+def rms_norm(x, weight, eps):
+    x = _f32(x)
+    out = np.empty_like(x)
+    w = None if weight is None else _f32(weight)
+    _check(lib().or_rms_norm(x.ctypes.data, x.size, None if w is None else w.ctypes.data,
+                             0 if w is None else w.size, eps, out.ctypes.data))
+    return out
+
+
+def rope_neox(x, position, base, n_rot, freq_factors=None):
+    x = _f32(x).copy()
+    f = None if freq_factors is None else _f32(freq_factors)
+    _check(lib().or_rope_neox(x.ctypes.data, x.size, position, base, n_rot,
+                              None if f is None else f.ctypes.data, 0 if f is None else f.size))
+    return x
+
+
+def norm_heads(x, head_dim, weight, eps):
+    x = _f32(x).copy()
+    w = None if weight is None else _f32(weight)
+    _check(lib().or_norm_heads(x.ctypes.data, x.size, head_dim, None if w is None else w.ctypes.data, eps))
+    return x
+
+
+def rope_heads(x, head_dim, position, base, freq_factors=None):
+    x = _f32(x).copy()
+    f = None if freq_factors is None else _f32(freq_factors)
+    _check(lib().or_rope_heads(x.ctypes.data, x.size, head_dim, position, base,
+                               None if f is None else f.ctypes.data, 0 if f is None else f.size))
+    return x
+
+
+def attend(q, keys, values, n_heads, n_kv_heads, scale=1.0):
+    """attend over a contiguous [T][n_kv*head_dim] image (model.rs:348-366)."""
+    q, keys, values = _f32(q), _f32(keys), _f32(values)
+    head_dim = q.size // n_heads
+    T = keys.size // (n_kv_heads * head_dim) if head_dim else 0
+    out = np.zeros(q.size, dtype=np.float32)
+    _check(lib().or_attend(q.ctypes.data, q.size, keys.ctypes.data, values.ctypes.data, T, n_heads, n_kv_heads,
+                           scale, out.ctypes.data))
+    return out
+
+
+def attend_rows(q, keys, values, n_heads, n_kv_heads, scale=1.0, threads=0):
+    """attend with the reference's per-row `concat` copy and head pool."""
+    q, keys, values = _f32(q), _f32(keys), _f32(values)
+    T = keys.shape[0]
+    kr = (c_vp * T)(*[keys[t].ctypes.data for t in range(T)])
+    vr = (c_vp * T)(*[values[t].ctypes.data for t in range(T)])
+    out = np.zeros(q.size, dtype=np.float32)
+    _check(lib().or_attend_rows(q.ctypes.data, q.size, kr, vr, T, n_heads, n_kv_heads, scale, threads,
+                                out.ctypes.data))
+    return out
+
+
+class RowPointers:
+    """Row pointer arrays for or_attend_rows over a large contiguous cache,
+    built once so that timing loops measure only the attention call."""
+
+    def __init__(self, keys, values):
+        self.keys, self.values = keys, values
+        T, w = keys.shape
+        kb, vb = keys.ctypes.data, values.ctypes.data
+        self.k = (c_vp * T)(*[kb + 4 * w * t for t in range(T)])
+        self.v = (c_vp * T)(*[vb + 4 * w * t for t in range(T)])
+        self.T = T
+
+    def attend(self, q, begin, end, n_heads, n_kv_heads, out, scale=1.0, threads=0):
+        kp = ctypes.cast(ctypes.byref(self.k, 8 * begin), ctypes.c_void_p)
+        vp = ctypes.cast(ctypes.byref(self.v, 8 * begin), ctypes.c_void_p)
+        _check(lib().or_attend_rows(q.ctypes.data, q.size, kp, vp, end - begin, n_heads, n_kv_heads, scale,
+                                    threads, out.ctypes.data))
+        return out
+
+
+def attend_f64(q, keys, values, n_heads, n_kv_heads, scale=1.0):
+    q, keys, values = _f32(q), _f32(keys), _f32(values)
+    head_dim = q.size // n_heads
+    T = keys.size // (n_kv_heads * head_dim)
+    out = np.zeros(q.size, dtype=np.float64)
+    _check(lib().or_attend_f64(q.ctypes.data, q.size, keys.ctypes.data, values.ctypes.data, T, n_heads,
+                               n_kv_heads, scale, out.ctypes.data))
+    return out
+
+
+def layer_attention_kind(n_layers, layer):
+    return "global" if lib().or_layer_attention_kind(n_layers, layer) else "local"
+
+
+def head_dim(n_layers, layer, local, glob):
+    return lib().or_head_dim(n_layers, layer, local, glob)
+
+
+def proportional_rope_freq_factors(hd, p):
+    out = np.zeros(hd // 2, dtype=np.float32)
+    lib().or_proportional_rope_freq_factors(hd, p, out.ctypes.data)
+    return out
+
+
+def windowed_len(seq_len, window):
+    b, e = c_size(0), c_size(0)
+    lib().or_windowed_len(seq_len, window, ctypes.byref(b), ctypes.byref(e))
+    return range(b.value, e.value)
+
+
+def kv_source_layer(n_layers, shared, layer):
+    out = c_size(0)
+    _check(lib().or_kv_source_layer(n_layers, shared, layer, ctypes.byref(out)))
+    return out.value
+
+
+class KvCache:
+    """The oracle's ContextMemory (context_memory.rs:21-86)."""
+
+    def __init__(self):
+        self.h = lib().or_kv_new()
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().or_kv_free(self.h)
+            self.h = None
+
+    def append(self, layer, k, v):
+        k, v = _f32(k), _f32(v)
+        _check(lib().or_kv_append(self.h, layer, k.ctypes.data, v.ctypes.data, k.size))
+
+    def view(self, layer, length):
+        kp, vp, w = c_vp(), c_vp(), c_size(0)
+        _check(lib().or_kv_view(self.h, layer, length, ctypes.byref(kp), ctypes.byref(vp), ctypes.byref(w)))
+        if length == 0:
+            return np.zeros((0, w.value), np.float32), np.zeros((0, w.value), np.float32)
+        n = length * w.value
+        k = np.ctypeslib.as_array(ctypes.cast(kp, P_f32), shape=(n,)).reshape(length, w.value).copy()
+        v = np.ctypeslib.as_array(ctypes.cast(vp, P_f32), shape=(n,)).reshape(length, w.value).copy()
+        return k, v
+
+    def clear(self):
+        lib().or_kv_clear(self.h)
+
+    def layer_attention(self, hp, layer, position, q, k, v, q_norm_w, k_norm_w, rope_freqs):
+        """Returns (out, source_layer, range) and leaves q/k/v normalised+rotated."""
+        q, k, v = _f32(q).copy(), _f32(k).copy(), _f32(v).copy()
+        qn = None if q_norm_w is None else _f32(q_norm_w)
+        kn = None if k_norm_w is None else _f32(k_norm_w)
+        rf = None if rope_freqs is None else _f32(rope_freqs)
+        out = np.zeros(q.size, np.float32)
+        src, b, e = c_size(0), c_size(0), c_size(0)
+        _check(lib().or_layer_attention(self.h, ctypes.byref(hp), layer, position, q.ctypes.data, k.ctypes.data,
+                                        v.ctypes.data, None if qn is None else qn.ctypes.data,
+                                        None if kn is None else kn.ctypes.data,
+                                        None if rf is None else rf.ctypes.data, 0 if rf is None else rf.size,
+                                        out.ctypes.data, ctypes.byref(src), ctypes.byref(b), ctypes.byref(e)))
+        return out, src.value, range(b.value, e.value), q, k, v
+
+
+def pool_threads():
+    return lib().or_pool_threads()
+
+
+def prepare_rows(x, head_dim, weight=None, eps=1e-6, pos0=0, base=0.0, freq_factors=None):
+    """In place on a C-contiguous float32 [n_rows, row_width] array: per-head
+    RMS norm, then (base > 0) NEOX RoPE at position pos0 + row."""
+    assert x.dtype == np.float32 and x.flags["C_CONTIGUOUS"]
+    w = None if weight is None else _f32(weight)
+    f = None if freq_factors is None else _f32(freq_factors)
+    _check(lib().or_prepare_rows(x.ctypes.data, x.shape[0], x.shape[1], head_dim,
+                                 None if w is None else w.ctypes.data, eps, pos0, base,
+                                 None if f is None else f.ctypes.data, 0 if f is None else f.size))
+    return x

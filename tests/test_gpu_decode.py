@@ -1,0 +1,184 @@
+"""Decode attention on the GPU against the oracle, through the C ABI.
+
+Tolerance (floating point): max |gpu - oracle| <= 1e-4 * max(|gpu|, |oracle|, 1),
+the reference's own assert_relative_eq (crates/llm-gemma4/tests/synthetic_generate.rs:74-83).
+The attended index set is checked exactly where the caller derives it.
+"""
+import numpy as np
+import pytest
+import torch
+
+import g4hip
+import inputs as I
+from oracle import pyoracle as orc
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def run_decode(ctx, q, K, V, begin, end, n_heads, n_kv, d, scale=1.0):
+    out = torch.zeros(n_heads * d, device="cuda")
+    ctx.attend_decode(dev(q), dev(K), dev(V), begin, end, n_heads, n_kv, d, out, scale=scale)
+    ctx.check_status()
+    return out.cpu().numpy()
+
+
+@pytest.mark.parametrize("name,T,d,glob", [("config1_sliding_ctx64", 64, 256, False),
+                                           ("config2_global_ctx4096", 4096, 512, True)])
+def test_measured_decode_configs(ctx, name, T, d, glob):
+    print(f"[case] {name}", flush=True)
+    q, K, V, _ = I.decode_case(1000 + T, T, d, glob)
+    begin, end = I.attended_range(T - 1, 0 if glob else I.WINDOW)
+    assert (begin, end) == (0, T)
+    out = run_decode(ctx, q, K, V, begin, end, 8, 1, d)
+    ref = orc.attend(q, K[begin:end], V[begin:end], 8, 1)
+    floor = np.max(np.abs(ref - orc.attend_f64(q, K[begin:end], V[begin:end], 8, 1)))
+    err = I.rel_err(out, ref)
+    print(f"[parity] {name}: rel err {err:.2e} (f32-vs-f64 floor of the oracle {floor:.2e})")
+    assert err <= TOL
+
+
+@pytest.mark.parametrize("d", [256, 512])
+@pytest.mark.parametrize("T", [1, 2, 15, 16, 17, 33, 100, 511, 512, 513, 1000])
+def test_decode_lengths(ctx, d, T):
+    q, K, V, _ = I.decode_case(7 * T + d, T, d, d == 512)
+    out = run_decode(ctx, q, K, V, 0, T, 8, 1, d)
+    assert I.rel_err(out, orc.attend(q, K, V, 8, 1)) <= TOL
+
+
+@pytest.mark.parametrize("chunk", [16, 32, 48, 256, 4096])
+def test_decode_split_counts(ctx, chunk):
+    """Split-K partials merge to the same result for any split size."""
+    T, d = 3000, 512
+    q, K, V, _ = I.decode_case(55, T, d, True)
+    ctx.set_decode_chunk(chunk)
+    try:
+        out = run_decode(ctx, q, K, V, 0, T, 8, 1, d)
+    finally:
+        ctx.set_decode_chunk(0)
+    assert I.rel_err(out, orc.attend(q, K, V, 8, 1)) <= TOL
+
+
+def test_sliding_window_inside_longer_cache(ctx):
+    """A sliding layer at position 1000 reads rows 489..1000 of its full-history cache."""
+    d, pos = 256, 1000
+    K, V = I.kv_rows(77, pos + 1, d, I.LOCAL_BASE, None)
+    q = I.queries(78, 1, d, I.LOCAL_BASE, None, pos)[0]
+    begin, end = I.attended_range(pos, I.WINDOW)
+    assert range(begin, end) == orc.windowed_len(pos + 1, 512) == range(489, 1001)
+    K[begin] = q[:d]  # the first row inside the window dominates head 0's softmax
+    K[:begin] = np.nan  # rows outside the window must never be read
+    V[:begin] = np.nan
+    out = run_decode(ctx, q, K, V, begin, end, 8, 1, d)
+    ref = orc.attend(q, K[begin:end], V[begin:end], 8, 1)
+    assert I.rel_err(out, ref) <= TOL
+    # so a window one row short is a clearly different answer
+    short = orc.attend(q, K[begin + 1:end], V[begin + 1:end], 8, 1)
+    assert I.rel_err(short, ref) > 0.1
+
+
+@pytest.mark.parametrize("n_heads,n_kv,d,T", [(4, 2, 8, 5), (4, 2, 16, 9), (8, 1, 64, 300), (2, 2, 16, 16),
+                                              (16, 2, 256, 200), (6, 4, 32, 7)])
+def test_other_shapes(ctx, n_heads, n_kv, d, T):
+    rng = np.random.default_rng(n_heads * 1000 + d + T)
+    q = rng.standard_normal(n_heads * d).astype(np.float32)
+    K = rng.standard_normal((T, n_kv * d)).astype(np.float32)
+    V = rng.standard_normal((T, n_kv * d)).astype(np.float32)
+    out = run_decode(ctx, q, K, V, 0, T, n_heads, n_kv, d, scale=0.3)
+    assert I.rel_err(out, orc.attend(q, K, V, n_heads, n_kv, 0.3)) <= TOL
+
+
+def test_host_attend_mirror(ctx):
+    """g4_attend takes the same arguments as the reference's attend (model.rs:348)."""
+    q, K, V, _ = I.decode_case(5, 200, 256, False)
+    out = ctx.attend(q, K, V, 8, 1, 1.0)
+    assert I.rel_err(out, orc.attend(q, K, V, 8, 1)) <= TOL
+    rng = np.random.default_rng(2)
+    q2 = rng.standard_normal(4 * 16).astype(np.float32)
+    K2 = rng.standard_normal((7, 2 * 16)).astype(np.float32)
+    V2 = rng.standard_normal((7, 2 * 16)).astype(np.float32)
+    assert I.rel_err(ctx.attend(q2, K2, V2, 4, 2, 1.0), orc.attend(q2, K2, V2, 4, 2)) <= TOL
+
+
+@pytest.mark.parametrize("d", [256, 512, 16])
+def test_non_finite_softmax_is_an_error(ctx, d):
+    n_kv = 1
+    T = 40
+    rng = np.random.default_rng(3)
+    q = rng.standard_normal(8 * d).astype(np.float32)
+    K = rng.standard_normal((T, d)).astype(np.float32)
+    V = rng.standard_normal((T, d)).astype(np.float32)
+    for poison in ("q_nan", "k_inf"):
+        q2, K2 = q.copy(), K.copy()
+        if poison == "q_nan":
+            q2[5] = np.nan
+        else:
+            K2[17, 3] = np.inf
+        with pytest.raises(orc.OracleError, match="softmax input is not finite"):
+            orc.attend(q2, K2, V, 8, n_kv)
+        out = torch.zeros(8 * d, device="cuda")
+        ctx.attend_decode(dev(q2), dev(K2), dev(V), 0, T, 8, n_kv, d, out)
+        with pytest.raises(g4hip.EngError, match="softmax input is not finite") as e:
+            ctx.check_status()
+        assert e.value.kind == "Compute"
+    # the status is cleared once reported
+    ctx.attend_decode(dev(q), dev(K), dev(V), 0, T, 8, n_kv, d, torch.zeros(8 * d, device="cuda"))
+    ctx.check_status()
+
+
+def test_empty_context_is_an_error(ctx):
+    with pytest.raises(g4hip.EngError, match="softmax input is not finite"):
+        ctx.attend(np.ones(8 * 256, np.float32), np.zeros((0, 256), np.float32), np.zeros((0, 256), np.float32),
+                   8, 1, 1.0)
+
+
+@pytest.mark.parametrize("d,glob", [(512, True), (256, False)])
+def test_ragged_batch_config5(ctx, d, glob):
+    """32 sequences, lengths U[1024, 32768], one launch (configuration 5)."""
+    print(f"[case] ragged batch d={d}", flush=True)
+    lens = I.ragged_lengths(2024)
+    B = lens.size
+    freqs = I.rope_freqs(99, d) if glob else None
+    base = I.GLOBAL_BASE if glob else I.LOCAL_BASE
+    row0 = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int64)
+    total = int(lens.sum())
+    # every sequence's own cache, packed one after another
+    begin = np.array([I.attended_range(int(L) - 1, 0 if glob else I.WINDOW)[0] for L in lens], np.int64)
+    end = lens.copy()
+    # Rows a sequence does not attend hold NaN: reading one would poison the result.
+    K = np.full((total, d), np.nan, np.float32)
+    V = np.full((total, d), np.nan, np.float32)
+    for s in range(B):
+        n = int(end[s] - begin[s])
+        k, v = I.kv_rows(3000 + s, n, d, base, freqs, pos0=int(begin[s]))
+        K[row0[s] + begin[s]:row0[s] + end[s]] = k
+        V[row0[s] + begin[s]:row0[s] + end[s]] = v
+    q = np.stack([I.queries(5000 + s, 1, d, base, freqs, int(lens[s]) - 1)[0] for s in range(B)])
+    out = torch.zeros(B * 8 * d, device="cuda")
+    ctx.attend_decode_batch(dev(q), dev(K), dev(V), dev(row0), dev(begin), dev(end), int((end - begin).max()),
+                            8, 1, d, out)
+    ctx.check_status()
+    got = out.cpu().numpy().reshape(B, -1)
+    worst = 0.0
+    for s in range(B):
+        rows = slice(row0[s] + begin[s], row0[s] + end[s])
+        worst = max(worst, I.rel_err(got[s], orc.attend(q[s], K[rows], V[rows], 8, 1)))
+    print(f"[parity] ragged d={d}: worst rel err {worst:.2e}")
+    assert worst <= TOL
+
+
+def test_ragged_range_longer_than_bound_is_reported(ctx):
+    d = 256
+    K, V = I.kv_rows(1, 64, d, I.LOCAL_BASE, None)
+    q = I.queries(2, 2, d, I.LOCAL_BASE, None, 63)
+    out = torch.zeros(2 * 8 * d, device="cuda")
+    begin = np.array([0, 0], np.int64)
+    end = np.array([64, 10], np.int64)
+    ctx.attend_decode_batch(dev(q), dev(K), dev(V), None, dev(begin), dev(end), 32, 8, 1, d, out)
+    with pytest.raises(g4hip.EngError) as e:
+        ctx.check_status()
+    assert e.value.kind == "ContextTooLong"

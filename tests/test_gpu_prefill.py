@@ -1,0 +1,80 @@
+"""Chunked prefill on the GPU against the oracle.
+
+The reference has no batched prefill: a prompt runs one token at a time
+(crates/llm-gemma4/src/impl_/generate.rs:37-41), so query i of a chunk must
+equal the oracle's attend over exactly the rows a decode at position
+pos0 + i sees (eng/mod.rs:10-36).  Tolerance as for decode: 1e-4 relative
+(crates/llm-gemma4/tests/synthetic_generate.rs:74-83).
+"""
+import numpy as np
+import pytest
+import torch
+
+import inputs as I
+from oracle import pyoracle as orc
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def prefill(ctx, q, K, V, pos0, N, window, d):
+    out = torch.zeros(N * 8 * d, device="cuda")
+    ctx.attend_prefill(dev(q), dev(K), dev(V), pos0, N, window, 8, 1, d, out)
+    ctx.check_status()
+    return out.cpu().numpy().reshape(N, 8 * d)
+
+
+def case(seed, rows, d, glob):
+    freqs = I.rope_freqs(seed + 1, d) if glob else None
+    base = I.GLOBAL_BASE if glob else I.LOCAL_BASE
+    K, V = I.kv_rows(seed, rows, d, base, freqs)
+    q = I.queries(seed + 2, rows, d, base, freqs, 0)
+    return q, K, V
+
+
+@pytest.mark.parametrize("d,window", [(256, 8), (256, 0), (512, 0), (512, 5), (256, 512)])
+@pytest.mark.parametrize("pos0,N", [(0, 40), (17, 23)])
+def test_prefill_every_query(ctx, d, window, pos0, N):
+    q, K, V = case(11 + d + window, pos0 + N, d, d == 512)
+    got = prefill(ctx, q[pos0:], K, V, pos0, N, window, d)
+    for i in range(N):
+        b, e = I.attended_range(pos0 + i, window)
+        assert I.rel_err(got[i], orc.attend(q[pos0 + i], K[b:e], V[b:e], 8, 1)) <= TOL, i
+
+
+@pytest.mark.parametrize("name,d,window", [("config4_sliding_W512", 256, 512), ("config4_global", 512, 0)])
+def test_config4_prefill_2048(ctx, name, d, window):
+    """2048-token prompt; every window/causal boundary row plus a seeded sample."""
+    print(f"[case] {name}", flush=True)
+    N = 2048
+    q, K, V = case(4000 + d, N, d, d == 512)
+    got = prefill(ctx, q, K, V, 0, N, window, d)
+    rows = sorted(set([0, 1, 2, 15, 16, 17, 510, 511, 512, 513, 1023, 1024, 1535, 2046, 2047]) |
+                  set(np.random.default_rng(8).integers(0, N, 96).tolist()))
+    worst = 0.0
+    for i in rows:
+        b, e = I.attended_range(i, window)
+        worst = max(worst, I.rel_err(got[i], orc.attend(q[i], K[b:e], V[b:e], 8, 1)))
+    print(f"[parity] {name}: worst rel err {worst:.2e} over {len(rows)} rows")
+    assert worst <= TOL
+    assert np.all(np.isfinite(got))
+
+
+def test_prefill_never_reads_future_or_out_of_window_rows(ctx):
+    """Rows after the chunk and before the first window hold NaN."""
+    d, W, pos0, N = 256, 64, 200, 50
+    q, K, V = case(5, pos0 + N + 30, d, False)
+    K[pos0 + N:] = np.nan
+    V[pos0 + N:] = np.nan
+    first = I.attended_range(pos0, W)[0]
+    K[:first] = np.nan
+    V[:first] = np.nan
+    got = prefill(ctx, q[pos0:pos0 + N], K, V, pos0, N, W, d)
+    assert np.all(np.isfinite(got))
+    for i in (0, 1, N // 2, N - 1):
+        b, e = I.attended_range(pos0 + i, W)
+        assert I.rel_err(got[i], orc.attend(q[pos0 + i], K[b:e], V[b:e], 8, 1)) <= TOL
