@@ -64,6 +64,19 @@ int ensure_workspace(g4_ctx *ctx, size_t bytes, hipStream_t stream) {
     return G4_OK;
 }
 
+int ensure_zero_rows(g4_ctx *ctx, int64_t n) {
+    if (ctx->zero_rows_len >= n) return G4_OK;
+    G4_HIP(hipDeviceSynchronize());
+    if (ctx->zero_rows) G4_HIP(hipFree(ctx->zero_rows));
+    ctx->zero_rows = nullptr;
+    ctx->zero_rows_len = 0;
+    const int64_t len = n < 1024 ? 1024 : n;
+    G4_HIP(hipMalloc(&ctx->zero_rows, len * sizeof(int64_t)));
+    G4_HIP(hipMemset(ctx->zero_rows, 0, len * sizeof(int64_t)));
+    ctx->zero_rows_len = len;
+    return G4_OK;
+}
+
 }  // namespace g4
 
 // -------------------------------------------------------------- device KvCache
@@ -115,6 +128,7 @@ int g4_release(g4_ctx *ctx) {
         G4_HIP(hipSetDevice(ctx->device));
         G4_HIP(hipDeviceSynchronize());
         if (ctx->ws.ptr) G4_HIP(hipFree(ctx->ws.ptr));
+        if (ctx->zero_rows) G4_HIP(hipFree(ctx->zero_rows));
         if (ctx->status_dev) G4_HIP(hipFree(ctx->status_dev));
         delete ctx;
         return (int)G4_OK;

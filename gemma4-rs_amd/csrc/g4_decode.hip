@@ -14,13 +14,15 @@
 // scores of keys 4g..4g+3 for head c -- exactly the B operand the P.V MFMA
 // needs for k-step r = keys {4g + r}, so P never moves between lanes.
 //
-// A workgroup is 4 wavefronts that split the head dimension: wave w owns dims
-// [w*D/4, (w+1)*D/4) of K, V, q and the output.  Each wave computes a partial
-// S^T over its dims; the four partials are summed through LDS (fixed order, so
-// every wave sees bit-identical scores and softmax state), then each wave
+// A workgroup is D/64 wavefronts that split the head dimension: wave w owns
+// dims [64w, 64w+64) of K, V, q and the output.  Each wave computes a partial
+// S^T over its dims; the partials are summed through LDS in a fixed order, so
+// every wave sees bit-identical scores and softmax state, then each wave
 // accumulates P.V for its own dims.  Work is split over keys (split-K): a
-// workgroup handles `chunk` consecutive keys of one (sequence, KV head) and
-// leaves an online-softmax partial (m, l, O) that a second kernel merges.
+// workgroup handles a power-of-two run of keys of one (sequence, KV head),
+// streaming 16-key tiles through a ring of register buffers (loads of the
+// next tiles in flight while the current one is computed), and leaves an
+// online-softmax partial (m, l, O) that a second kernel merges.
 //
 // Softmax semantics follow softmax_f32 (crates/llm-backend-cpu/src/ops.rs:105-127):
 // p = exp(s - max) / sum with scale applied to the dot product first
@@ -35,7 +37,8 @@ namespace {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kMaxSplits = 1024;  // per (sequence, KV head); bounds the merge's LDS table
+constexpr int kDecodeBuffers = 3;  // K/V tiles held per wave (NBUF-1 in flight)
+constexpr int kMaxSplits = 512;  // per (sequence, KV head); bounds the merge's LDS table
 
 struct DecodeK {
     const float *q;
@@ -49,73 +52,130 @@ struct DecodeK {
     int64_t pos0, prefill_window;
     int n_heads, n_kv_heads, group;
     float scale;
-    int64_t chunk;
+    int chunk_shift;  // keys per split = 1 << chunk_shift
     int max_splits;
     float *out;
-    float *part_o;   // [B][n_kv][max_splits][group][D]
+    float *part_o;   // per (sequence, KV head, split): D*G floats, accumulator layout
     float2 *part_ml; // [B][n_kv][max_splits][group]  (running max, sum of exp)
     unsigned *status;
 };
 
+// How a launch names each sequence's rows.  The form is a template parameter
+// so that the kernels' prologues load their arguments without data-dependent
+// branches (each dependent scalar load is a memory round trip).
+enum Mode : int {
+    kSingle = 0,  // one sequence: rows [kv_begin0, kv_end0)
+    kBatch = 1,   // B sequences: rows [kv_begin[s], kv_end[s]) of a cache starting at row seq_row0[s]
+    kPrefill = 2  // N queries of one sequence at positions pos0 + s (causal / windowed)
+};
+
 // Rows [begin, end) that sequence s attends, and where its cache starts.
+template <int MODE>
 __device__ inline void seq_range(const DecodeK &p, int s, int64_t &row0, int64_t &begin,
                                  int64_t &end) {
-    if (p.prefill_window >= 0) {  // query s sits at position pos0 + s
+    if constexpr (MODE == kPrefill) {
         end = p.pos0 + s + 1;
         begin = (p.prefill_window > 0 && end > p.prefill_window) ? end - p.prefill_window : 0;
         row0 = 0;
+    } else if constexpr (MODE == kBatch) {
+        row0 = p.seq_row0[s];
+        begin = p.kv_begin[s];
+        end = p.kv_end[s];
     } else {
-        row0 = p.seq_row0 ? p.seq_row0[s] : 0;
-        begin = p.kv_begin ? p.kv_begin[s] : p.kv_begin0;
-        end = p.kv_end ? p.kv_end[s] : p.kv_end0;
+        row0 = 0;
+        begin = p.kv_begin0;
+        end = p.kv_end0;
     }
 }
 
 __device__ inline int64_t num_splits(const DecodeK &p, int64_t len) {
-    int64_t n = (len + p.chunk - 1) / p.chunk;
+    const int64_t n = (len + (1LL << p.chunk_shift) - 1) >> p.chunk_shift;
     return n < p.max_splits ? n : p.max_splits;
 }
 
 __device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// One workgroup = one (split, KV head, sequence).  D = head_dim (256 or 512).
-template <int D>
-__global__ __launch_bounds__(256) void decode_split_kernel(DecodeK p) {
-    constexpr int DW = D / 4;   // dims owned by one wave
-    constexpr int NU = DW / 32; // 32-dim K chunks per wave (8 MFMA k-steps each)
-    constexpr int NV = DW / 64; // 64-dim V groups per wave (4 output tiles each)
-    constexpr int NT = DW / 16; // 16-dim output tiles per wave
-    static_assert(D % 256 == 0, "head_dim must be a multiple of 256");
+// One 16-key tile of K and V in registers, in the MFMA operand layouts of
+// lane (g, c): K rows t0 + c, dims base + 32u + 8g .. +7 (A of S^T = K.Q^T);
+// V rows t0 + 4g + r, dims base + 4c .. +3 (A of O^T = V^T.P^T).
+struct KvTile {
+    f32x4 k[2][2];
+    f32x4 v[4];
+};
 
+// Split partials are stored in the accumulator layout, so every lane writes
+// whole 16-byte vectors: for wave w, output tile i, lane group g and head c,
+// the four rows r of O^T (dims w*64 + 16g + 4r + i) are one f32x4 at
+// element ((w*4 + i)*4 + g)*G + c of the split's D*G/4 vectors.
+__device__ inline int partial_dim(int e, int G) {
+    const int g = (e / G) & 3, i = (e / (4 * G)) & 3, w = e / (16 * G);
+    return w * 64 + 16 * g + i;  // + 4r for component r
+}
+
+// One workgroup = one (split, KV head, sequence); NW wavefronts, each owning
+// 64 of the D = 64*NW head dims.  Tiles of 16 keys are software-pipelined
+// through NBUF register buffers: loads are issued unconditionally (clamped
+// rows), so the compiler's wait counts stay exact and never wait on a
+// prefetch.
+template <int NW, int MODE, int NBUF, int MINB = 1>
+__global__ __launch_bounds__(64 * NW, MINB) void decode_split_kernel(DecodeK p) {
+    constexpr int D = 64 * NW;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, c = lane & 15;
     const int split = blockIdx.x, kvh = blockIdx.y, s = blockIdx.z;
 
     int64_t row0, begin, end;
-    seq_range(p, s, row0, begin, end);
+    seq_range<MODE>(p, s, row0, begin, end);
     const int64_t len = end - begin;
-    if (len <= 0 || len > p.max_kv_len) {
+    if (MODE != kSingle && (len <= 0 || len > p.max_kv_len)) {  // kSingle: checked by the host
         if (split == 0 && kvh == 0 && threadIdx.x == 0)
             atomicOr(p.status, len <= 0 ? kStatusNonFinite : kStatusRangeTooLong);
         return;
     }
-    const int64_t n_splits = num_splits(p, len);
+    const int64_t n_splits = MODE == kSingle ? p.max_splits : num_splits(p, len);
     if (split >= n_splits) return;
-    const int64_t k_lo = begin + split * p.chunk;
-    const int64_t k_hi = (split + 1 == n_splits) ? end : k_lo + p.chunk;
+    const int64_t k_lo = begin + ((int64_t)split << p.chunk_shift);
+    const int64_t k_hi = (split + 1 == n_splits) ? end : k_lo + (1LL << p.chunk_shift);
 
-    const int base = wave * DW;
+    const int base = wave * 64;
     const bool col_valid = c < p.group;
     const int head = kvh * p.group + (col_valid ? c : 0);
+    const float *kcol = p.k + row0 * p.row_stride + (int64_t)kvh * D + base + 8 * g;
+    const float *vcol = p.v + row0 * p.row_stride + (int64_t)kvh * D + base + 4 * c;
+    const int stride = (int)p.row_stride;  // fits: checked by the launcher
+
+    // Rows past k_hi are clamped to k_hi - 1 (loaded, then masked).
+    auto load_tile = [&](int64_t t0, KvTile &T) {
+        const int last = (int)(k_hi - 1 - t0);
+        const float *kt = kcol + t0 * p.row_stride;
+        const float *kp = kt + (c < last ? c : last) * stride;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            T.k[u][0] = *(const f32x4 *)(kp + 32 * u);
+            T.k[u][1] = *(const f32x4 *)(kp + 32 * u + 4);
+        }
+        const float *vt = vcol + t0 * p.row_stride;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int rv = 4 * g + r;
+            T.v[r] = *(const f32x4 *)(vt + (rv < last ? rv : last) * stride);
+        }
+    };
+
+    // Ring of NBUF tiles: NBUF-1 tiles are in flight while one is computed.
+    const int n_tiles = (int)((k_hi - k_lo + 15) >> 4);
+    KvTile T[NBUF];
+#pragma unroll
+    for (int b = 0; b < NBUF - 1; ++b) load_tile(k_lo + 16 * (b < n_tiles ? b : n_tiles - 1), T[b]);
 
     // Q^T as the B operand: lane (g, c) holds q[head c][base + 32u + 8g + j].
-    float qreg[NU][8];
+    float qreg[2][8];
     {
         const float *qh = p.q + ((int64_t)s * p.n_heads + head) * D + base + 8 * g;
 #pragma unroll
-        for (int u = 0; u < NU; ++u) {
-            f32x4 a = *(const f32x4 *)(qh + 32 * u);
-            f32x4 b = *(const f32x4 *)(qh + 32 * u + 4);
+        for (int u = 0; u < 2; ++u) {
+            const f32x4 a = *(const f32x4 *)(qh + 32 * u);
+            const f32x4 b = *(const f32x4 *)(qh + 32 * u + 4);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 qreg[u][j] = col_valid ? a[j] : 0.0f;
@@ -124,59 +184,39 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeK p) {
         }
     }
 
-    const float *kcol = p.k + row0 * p.row_stride + (int64_t)kvh * D + base;
-    const float *vcol = p.v + row0 * p.row_stride + (int64_t)kvh * D + base;
-
-    __shared__ f32x4 sx[2][4][64];  // partial S^T exchange, double-buffered by iteration
+    __shared__ f32x4 sx[2][NW][64];  // partial S^T exchange, double-buffered
 
     float m = -INFINITY, l = 0.0f;
     bool bad = false;
-    f32x4 o[NT];
+    f32x4 o[4];
 #pragma unroll
-    for (int i = 0; i < NT; ++i) o[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = 0; i < 4; ++i) o[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    int buf = 0;
 
-    int it = 0;
-    for (int64_t t0 = k_lo; t0 < k_hi; t0 += 16, ++it) {
-        // K rows t0 + c (clamped into range; masked below), dims base+32u+8g..+7.
-        const int64_t tk = (t0 + c < k_hi) ? t0 + c : k_hi - 1;
-        const float *kp = kcol + tk * p.row_stride + 8 * g;
-        f32x4 kv[NU][2];
+    auto compute_tile = [&](int64_t t0, const KvTile &T) {
+        // Partial S^T over this wave's 64 dims, two independent MFMA chains.
+        f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int u = 0; u < NU; ++u) {
-            kv[u][0] = *(const f32x4 *)(kp + 32 * u);
-            kv[u][1] = *(const f32x4 *)(kp + 32 * u + 4);
+        for (int j = 0; j < 8; ++j) {
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(T.k[0][j >> 2][j & 3], qreg[0][j], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(T.k[1][j >> 2][j & 3], qreg[1][j], acc1, 0, 0, 0);
         }
-        // V rows t0 + 4g + r, dims base + 64U + 4c..+3.
-        f32x4 vv[4][NV];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int64_t tv = (t0 + 4 * g + r < k_hi) ? t0 + 4 * g + r : k_hi - 1;
-            const float *vp = vcol + tv * p.row_stride + 4 * c;
-#pragma unroll
-            for (int U = 0; U < NV; ++U) vv[r][U] = *(const f32x4 *)(vp + 64 * U);
-        }
-
-        // Partial S^T over this wave's dims.
-        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int u = 0; u < NU; ++u)
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[u][j >> 2][j & 3], qreg[u][j], acc, 0, 0, 0);
-
-        const int buf = it & 1;
-        sx[buf][wave][lane] = acc;
+        sx[buf][wave][lane] = acc0 + acc1;
         __syncthreads();
-        f32x4 sc = ((sx[buf][0][lane] + sx[buf][1][lane]) + sx[buf][2][lane]) + sx[buf][3][lane];
+        f32x4 sc = sx[buf][0][lane];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) sc += sx[buf][w][lane];
+        buf ^= 1;
 
         // Scores of keys t0 + 4g + r for head c; mask the tail.
         float sv[4];
         float mt = -INFINITY;
+        const int64_t valid = k_hi - t0;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            float x = sc[r] * p.scale;
+            const float x = sc[r] * p.scale;
             bad |= (x != x) || (x == INFINITY);
-            sv[r] = (t0 + 4 * g + r < k_hi) ? x : -INFINITY;
+            sv[r] = (4 * g + r < valid) ? x : -INFINITY;
             mt = fmaxf(mt, sv[r]);
         }
         mt = fmaxf(mt, __shfl_xor(mt, 16));
@@ -195,117 +235,179 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeK p) {
         l = l * alpha + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
         m = m_new;
 #pragma unroll
-        for (int i = 0; i < NT; ++i) o[i] *= alpha;
+        for (int i = 0; i < 4; ++i) o[i] *= alpha;
 
-        // O^T += V^T . P^T, k-step r covers keys {t0 + 4g + r}.
+        // O^T += V^T . P^T; k-step r covers keys {t0 + 4g + r}; tile i holds
+        // dims base + 4c' + i for output row c'.
 #pragma unroll
         for (int r = 0; r < 4; ++r)
 #pragma unroll
-            for (int U = 0; U < NV; ++U)
+            for (int i = 0; i < 4; ++i)
+                o[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(T.v[r][i], pr[r], o[i], 0, 0, 0);
+    };
+
+    // Steady state: each step issues the load of the tile NBUF-1 ahead
+    // (clamped into range, so every load is unconditional and the wait
+    // counts stay exact), then computes the oldest buffered tile.
+    int i = 0;
+    for (; i + NBUF - 1 < n_tiles; i += NBUF) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    o[4 * U + i] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[r][U][i], pr[r], o[4 * U + i], 0, 0, 0);
+        for (int b = 0; b < NBUF; ++b) {
+            const int pf = i + b + NBUF - 1;
+            load_tile(k_lo + 16 * (pf < n_tiles ? pf : n_tiles - 1), T[(b + NBUF - 1) % NBUF]);
+            compute_tile(k_lo + 16 * (i + b), T[b]);
+        }
     }
+    // Tail: the remaining (< NBUF) tiles are already buffered in T[0..].
+#pragma unroll
+    for (int b = 0; b < NBUF - 1; ++b)
+        if (i + b < n_tiles) compute_tile(k_lo + 16 * (i + b), T[b]);
 
     if (wave == 0 && __any(bad && col_valid) && lane == 0) atomicOr(p.status, kStatusNonFinite);
 
-    // Sum of exp over the whole split for head c (lanes c, c+16, c+32, c+48).
+    // Sum of exp over the split for head c (lanes c, c+16, c+32, c+48).
     float lt = l + __shfl_xor(l, 16);
     lt = lt + __shfl_xor(lt, 32);
 
     if (n_splits == 1) {
-        if (m == -INFINITY) {
-            if (wave == 0 && lane == 0) atomicOr(p.status, kStatusNonFinite);
-        }
+        if (m == -INFINITY && wave == 0 && lane == 0) atomicOr(p.status, kStatusNonFinite);
         if (!col_valid) return;
         const float inv = 1.0f / lt;
         float *op = p.out + ((int64_t)s * p.n_heads + head) * D + base;
 #pragma unroll
-        for (int U = 0; U < NV; ++U)
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) op[64 * U + 4 * (4 * g + r) + i] = o[4 * U + i][r] * inv;
+            for (int r = 0; r < 4; ++r) op[4 * (4 * g + r) + i] = o[i][r] * inv;
         return;
     }
     if (!col_valid) return;
     const int64_t slot = ((int64_t)s * p.n_kv_heads + kvh) * p.max_splits + split;
-    float *po = p.part_o + (slot * p.group + c) * D + base;
+    f32x4 *po = (f32x4 *)(p.part_o + slot * p.group * D);
 #pragma unroll
-    for (int U = 0; U < NV; ++U)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) po[64 * U + 4 * (4 * g + r) + i] = o[4 * U + i][r];
+    for (int i = 0; i < 4; ++i) po[((wave * 4 + i) * 4 + g) * p.group + c] = o[i];
     if (wave == 0 && g == 0) p.part_ml[slot * p.group + c] = float2{m, lt};
 }
 
-// Merges the split partials of one (sequence, head) for 64 dims:
-// O = sum_j e^(m_j - M) O_j / sum_j e^(m_j - M) l_j.
+// Merges the split partials of one (sequence, KV head):
+// O_c = sum_j e^(m_jc - M_c) O_jc / sum_j e^(m_jc - M_c) l_jc for each head c.
+// A workgroup covers 16 stored vectors x 16 split phases.  Every load it needs
+// -- its partial vectors and the (m, l) table -- is issued before any result
+// is used, so the merge costs about one memory round trip.  Phase sums are
+// added in a fixed order (deterministic).
+constexpr int kMergeBatch = 16;
+template <int MODE>
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeK p, int D) {
-    const int s = blockIdx.z, head = blockIdx.y;
+    const int s = blockIdx.z, kvh = blockIdx.y;
     const int tid = threadIdx.x;
-    int64_t row0, begin, end;
-    seq_range(p, s, row0, begin, end);
-    const int64_t len = end - begin;
-    if (len <= 0 || len > p.max_kv_len) return;
-    const int n = (int)num_splits(p, len);
+    int n = p.max_splits;
+    if constexpr (MODE != kSingle) {
+        int64_t row0, begin, end;
+        seq_range<MODE>(p, s, row0, begin, end);
+        const int64_t len = end - begin;
+        if (len <= 0 || len > p.max_kv_len) return;
+        n = (int)num_splits(p, len);
+    }
     if (n <= 1) return;
-    const int kvh = head / p.group, c = head % p.group;
+    const int G = p.group;
     const int64_t slot0 = ((int64_t)s * p.n_kv_heads + kvh) * p.max_splits;
 
-    __shared__ float w[kMaxSplits];
-    __shared__ float red[256];
-    __shared__ float part[4][64];
+    const int ph = tid >> 4, el = tid & 15;
+    const int e = blockIdx.x * 16 + el;  // stored vector index within a split
+    const int c = e % G;
+    const f32x4 *src = (const f32x4 *)(p.part_o + slot0 * G * D) + e;
+    const int64_t jstride = (int64_t)G * D / 4;
 
-    float mx = -INFINITY;
-    for (int j = tid; j < n; j += 256) mx = fmaxf(mx, p.part_ml[(slot0 + j) * p.group + c].x);
-    red[tid] = mx;
+    __shared__ float2 ml[kMaxSplits * 16];  // (m, l), then (weight, l)
+    __shared__ float red[16][16];
+    __shared__ float Mc[16], Lc[16];
+    __shared__ f32x4 part[16][16];
+
+    // All loads are unconditional (indices clamped into range) so that they
+    // issue back to back: the (m, l) table first, then the partial vectors.
+    const float2 *mlg = p.part_ml + slot0 * G;
+    const int nml = n * G;
+    float2 t[8];
+#pragma unroll
+    for (int b = 0; b < 8; ++b) t[b] = mlg[min(tid + 256 * b, nml - 1)];
+    f32x4 v[kMergeBatch];
+#pragma unroll
+    for (int b = 0; b < kMergeBatch; ++b) v[b] = src[min(ph + 16 * b, n - 1) * jstride];
+#pragma unroll
+    for (int b = 0; b < 8; ++b)
+        if (tid + 256 * b < nml) ml[tid + 256 * b] = t[b];
+    for (int i = tid + 256 * 8; i < nml; i += 256) ml[i] = mlg[i];
     __syncthreads();
-    for (int off = 128; off > 0; off >>= 1) {
-        if (tid < off) red[tid] = fmaxf(red[tid], red[tid + off]);
-        __syncthreads();
+    // M_c = max_j m_jc: thread (k, cc) scans splits j = k, k+16, ...
+    const int cc = tid & 15, k = tid >> 4;
+    float mx = -INFINITY;
+    if (cc < G)
+        for (int j = k; j < n; j += 16) mx = fmaxf(mx, ml[j * G + cc].x);
+    red[k][cc] = mx;
+    __syncthreads();
+    if (tid < 16) {
+        float mm = red[0][tid];
+        for (int q = 1; q < 16; ++q) mm = fmaxf(mm, red[q][tid]);
+        Mc[tid] = mm;
     }
-    const float M = red[0];
     __syncthreads();
     float lsum = 0.0f;
-    for (int j = tid; j < n; j += 256) {
-        float2 ml = p.part_ml[(slot0 + j) * p.group + c];
-        float wj = (ml.x == -INFINITY) ? 0.0f : exp2_fast((ml.x - M) * kLog2e);
-        w[j] = wj;
-        lsum += wj * ml.y;
+    if (cc < G) {
+        const float M = Mc[cc];
+        for (int j = k; j < n; j += 16) {
+            const float2 t = ml[j * G + cc];
+            const float w = (t.x == -INFINITY) ? 0.0f : exp2_fast((t.x - M) * kLog2e);
+            ml[j * G + cc].x = w;
+            lsum += w * t.y;
+        }
     }
-    red[tid] = lsum;
+    red[k][cc] = lsum;
     __syncthreads();
-    for (int off = 128; off > 0; off >>= 1) {
-        if (tid < off) red[tid] = red[tid] + red[tid + off];
-        __syncthreads();
+    if (tid < 16) {
+        float ls = red[0][tid];
+        for (int q = 1; q < 16; ++q) ls += red[q][tid];
+        Lc[tid] = ls;
+        if (tid < G && Mc[tid] == -INFINITY && blockIdx.x == 0) atomicOr(p.status, kStatusNonFinite);
     }
-    const float L = red[0];
-    if (M == -INFINITY && tid == 0 && blockIdx.x == 0) atomicOr(p.status, kStatusNonFinite);
+    __syncthreads();
 
-    // 4 phases x 16 lanes x 4 dims: phase ph sums splits j = ph, ph+4, ...
-    const int ph = tid >> 6, dl = tid & 63;
-    const int d = blockIdx.x * 64 + dl;
-    float acc = 0.0f;
-    if (d < D) {
-        for (int j = ph; j < n; j += 4) acc += w[j] * p.part_o[((slot0 + j) * p.group + c) * D + d];
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int b = 0; b < kMergeBatch; ++b) {
+        const int j = ph + 16 * b;
+        const float w = ml[min(j, n - 1) * G + c].x;
+        acc += (j < n ? w : 0.0f) * v[b];
     }
-    part[ph][dl] = acc;
+    for (int j0 = ph + 16 * kMergeBatch; j0 < n; j0 += 16 * kMergeBatch) {
+#pragma unroll
+        for (int b = 0; b < kMergeBatch; ++b) v[b] = src[min(j0 + 16 * b, n - 1) * jstride];
+#pragma unroll
+        for (int b = 0; b < kMergeBatch; ++b) {
+            const int j = j0 + 16 * b;
+            const float w = ml[min(j, n - 1) * G + c].x;
+            acc += (j < n ? w : 0.0f) * v[b];
+        }
+    }
+    part[ph][el] = acc;
     __syncthreads();
-    if (ph == 0 && d < D) {
-        const float sum = ((part[0][dl] + part[1][dl]) + part[2][dl]) + part[3][dl];
-        p.out[((int64_t)s * p.n_heads + head) * D + d] = sum / L;
+    if (ph == 0) {
+        f32x4 sum = part[0][el];
+#pragma unroll
+        for (int q = 1; q < 16; ++q) sum += part[q][el];
+        const float inv = 1.0f / Lc[c];
+        float *op = p.out + ((int64_t)s * p.n_heads + kvh * G + c) * D + partial_dim(e, G);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) op[4 * r] = sum[r] * inv;
     }
 }
 
 // Any shape the MFMA kernel does not cover (head_dim not a multiple of 256,
 // more than 16 query heads per KV head): one workgroup per (head, sequence),
 // 256 keys per step, online softmax in f32.
+template <int MODE>
 __global__ __launch_bounds__(256) void decode_generic_kernel(DecodeK p, int D) {
     const int head = blockIdx.x, s = blockIdx.y, tid = threadIdx.x;
     int64_t row0, begin, end;
-    seq_range(p, s, row0, begin, end);
+    seq_range<MODE>(p, s, row0, begin, end);
     const int64_t len = end - begin;
     if (len <= 0 || len > p.max_kv_len) {
         if (head == 0 && tid == 0) atomicOr(p.status, len <= 0 ? kStatusNonFinite : kStatusRangeTooLong);
@@ -375,10 +477,74 @@ __global__ __launch_bounds__(256) void decode_generic_kernel(DecodeK p, int D) {
 
 }  // namespace
 
+namespace {
+
+template <int MODE>
+int launch_mode(g4_ctx *ctx, const DecodeArgs &a, DecodeK p, hipStream_t stream) {
+    const int D = a.head_dim;
+    const int group = p.group;
+    const bool mfma = (D == 256 || D == 512) && group <= 16 && a.n_heads % a.n_kv_heads == 0 &&
+                      a.row_stride <= (1LL << 26);  // 16 rows of stride fit 32-bit offsets
+    if (!mfma) {
+        if (D > 1024) return set_error(G4_ERR_COMPUTE, "head_dim above 1024 is not supported");
+        p.chunk_shift = 62;
+        p.max_splits = 1;
+        hipLaunchKernelGGL(decode_generic_kernel<MODE>, dim3(a.n_heads, a.B), dim3(256),
+                           (size_t)(D + 256) * sizeof(float), stream, p, D);
+        G4_HIP(hipGetLastError());
+        return G4_OK;
+    }
+
+    // Split-K sizing.  A split is a power of two of at least one 16-key
+    // MFMA tile.  One sequence: about two workgroups per CU, at least 32
+    // keys each (a split's fixed cost -- its first loads and its partial --
+    // outweighs a smaller share).  Ragged batches: about eight per CU, so
+    // that sequences of very different lengths still balance over the CUs.
+    // Contexts of a few tiles run as one split (no merge).
+    const int64_t units = (int64_t)a.B * a.n_kv_heads;
+    const int64_t max_len = a.max_kv_len > 0 ? a.max_kv_len : 1;
+    int64_t chunk = ctx->decode_chunk;
+    if (chunk <= 0) {
+        const int64_t target = (MODE == kSingle ? 2LL : 8LL) * ctx->num_cus;
+        chunk = (max_len * units + target - 1) / target;
+        const int64_t floor_keys = MODE == kSingle ? 32 : 64;
+        if (chunk < floor_keys) chunk = floor_keys;
+        if (max_len <= 64) chunk = max_len;
+    }
+    const int64_t min_chunk = (max_len + kMaxSplits - 1) / kMaxSplits;
+    if (chunk < min_chunk) chunk = min_chunk;
+    int shift = 4;
+    while ((1LL << shift) < chunk) ++shift;
+    const int64_t max_splits = (max_len + (1LL << shift) - 1) >> shift;
+    p.chunk_shift = shift;
+    p.max_splits = (int)max_splits;
+    if (max_splits > 1) {
+        const size_t slots = (size_t)units * max_splits * group;
+        const size_t bytes = slots * D * sizeof(float) + slots * sizeof(float2) + 256;
+        int rc = ensure_workspace(ctx, bytes, stream);
+        if (rc != G4_OK) return rc;
+        p.part_o = (float *)ctx->ws.ptr;
+        size_t off = (slots * D * sizeof(float) + 255) / 256 * 256;
+        p.part_ml = (float2 *)((char *)ctx->ws.ptr + off);
+    }
+    dim3 grid((unsigned)max_splits, (unsigned)a.n_kv_heads, (unsigned)a.B);
+    if (D == 256)
+        hipLaunchKernelGGL((decode_split_kernel<4, MODE, kDecodeBuffers>), grid, dim3(256), 0, stream, p);
+    else
+        hipLaunchKernelGGL((decode_split_kernel<8, MODE, kDecodeBuffers>), grid, dim3(512), 0, stream, p);
+    G4_HIP(hipGetLastError());
+    if (max_splits > 1) {
+        hipLaunchKernelGGL(decode_merge_kernel<MODE>, dim3(D * group / 64, a.n_kv_heads, a.B), dim3(256), 0,
+                           stream, p, D);
+        G4_HIP(hipGetLastError());
+    }
+    return G4_OK;
+}
+
+}  // namespace
+
 int launch_decode(g4_ctx *ctx, const DecodeArgs &a, hipStream_t stream) {
     if (a.B <= 0) return G4_OK;
-    const int D = a.head_dim;
-    const int group = a.n_heads / a.n_kv_heads;
     DecodeK p{};
     p.q = a.q;
     p.k = a.k;
@@ -394,59 +560,20 @@ int launch_decode(g4_ctx *ctx, const DecodeArgs &a, hipStream_t stream) {
     p.prefill_window = a.prefill_window;
     p.n_heads = a.n_heads;
     p.n_kv_heads = a.n_kv_heads;
-    p.group = group;
+    p.group = a.n_heads / a.n_kv_heads;
     p.scale = a.scale;
     p.out = a.out;
     p.status = ctx->status_dev;
-
-    const bool mfma = (D == 256 || D == 512) && group <= 16 && a.n_heads % a.n_kv_heads == 0;
-    if (!mfma) {
-        if (D > 1024) return set_error(G4_ERR_COMPUTE, "head_dim above 1024 is not supported");
-        p.chunk = a.max_kv_len > 0 ? a.max_kv_len : 1;
-        p.max_splits = 1;
-        hipLaunchKernelGGL(decode_generic_kernel, dim3(a.n_heads, a.B), dim3(256),
-                           (size_t)(D + 256) * sizeof(float), stream, p, D);
-        G4_HIP(hipGetLastError());
-        return G4_OK;
+    if (a.prefill_window >= 0) return launch_mode<kPrefill>(ctx, a, p, stream);
+    if (a.kv_begin) {
+        if (!p.seq_row0) {  // a zero row offset for every sequence
+            int rc = ensure_zero_rows(ctx, a.B);
+            if (rc != G4_OK) return rc;
+            p.seq_row0 = ctx->zero_rows;
+        }
+        return launch_mode<kBatch>(ctx, a, p, stream);
     }
-
-    // Split-K sizing: enough (sequence, KV head, split) work items to give
-    // every CU a few workgroups, in multiples of the 16-key MFMA tile.
-    const int64_t units = (int64_t)a.B * a.n_kv_heads;
-    const int64_t max_len = a.max_kv_len > 0 ? a.max_kv_len : 1;
-    int64_t chunk = ctx->decode_chunk;
-    if (chunk <= 0) {
-        const int64_t target = 4LL * ctx->num_cus;
-        chunk = (max_len * units + target - 1) / target;
-    }
-    chunk = (chunk + 15) / 16 * 16;
-    if (chunk < 16) chunk = 16;
-    const int64_t min_chunk = (max_len + kMaxSplits - 1) / kMaxSplits;
-    if (chunk < min_chunk) chunk = (min_chunk + 15) / 16 * 16;
-    const int64_t max_splits = (max_len + chunk - 1) / chunk;
-    p.chunk = chunk;
-    p.max_splits = (int)max_splits;
-    if (max_splits > 1) {
-        const size_t slots = (size_t)units * max_splits * group;
-        const size_t bytes = slots * D * sizeof(float) + slots * sizeof(float2) + 256;
-        int rc = ensure_workspace(ctx, bytes, stream);
-        if (rc != G4_OK) return rc;
-        p.part_o = (float *)ctx->ws.ptr;
-        size_t off = (slots * D * sizeof(float) + 255) / 256 * 256;
-        p.part_ml = (float2 *)((char *)ctx->ws.ptr + off);
-    }
-    dim3 grid((unsigned)max_splits, (unsigned)a.n_kv_heads, (unsigned)a.B);
-    if (D == 256)
-        hipLaunchKernelGGL(decode_split_kernel<256>, grid, dim3(256), 0, stream, p);
-    else
-        hipLaunchKernelGGL(decode_split_kernel<512>, grid, dim3(256), 0, stream, p);
-    G4_HIP(hipGetLastError());
-    if (max_splits > 1) {
-        hipLaunchKernelGGL(decode_merge_kernel, dim3((D + 63) / 64, a.n_heads, a.B), dim3(256), 0,
-                           stream, p, D);
-        G4_HIP(hipGetLastError());
-    }
-    return G4_OK;
+    return launch_mode<kSingle>(ctx, a, p, stream);
 }
 
 }  // namespace g4

@@ -43,6 +43,8 @@ struct g4_ctx {
     g4::Workspace ws;                // split-K partials of the decode kernels
     int64_t decode_chunk = 0;        // 0 = automatic
     int num_cus = 256;
+    int64_t *zero_rows = nullptr;    // device zeros: default row offsets of a batch
+    int64_t zero_rows_len = 0;
 };
 
 namespace g4 {
@@ -50,6 +52,8 @@ namespace g4 {
 // Grows the context's workspace to at least `bytes` (stream-ordered users
 // must not be in flight on another stream when it grows).
 int ensure_workspace(g4_ctx *ctx, size_t bytes, hipStream_t stream);
+// Makes ctx->zero_rows hold at least n zero int64 values.
+int ensure_zero_rows(g4_ctx *ctx, int64_t n);
 
 // Launchers implemented in the .hip files.
 struct DecodeArgs {
