@@ -129,6 +129,7 @@ int g4_release(g4_ctx *ctx) {
         G4_HIP(hipDeviceSynchronize());
         if (ctx->ws.ptr) G4_HIP(hipFree(ctx->ws.ptr));
         if (ctx->zero_rows) G4_HIP(hipFree(ctx->zero_rows));
+        g4::release_prefill_plan(ctx);
         if (ctx->status_dev) G4_HIP(hipFree(ctx->status_dev));
         delete ctx;
         return (int)G4_OK;

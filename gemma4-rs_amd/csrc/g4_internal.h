@@ -45,6 +45,7 @@ struct g4_ctx {
     int num_cus = 256;
     int64_t *zero_rows = nullptr;    // device zeros: default row offsets of a batch
     int64_t zero_rows_len = 0;
+    void *prefill_plan = nullptr;    // work-unit table of the last prefill shape
 };
 
 namespace g4 {
@@ -88,6 +89,7 @@ struct PrefillArgs {
     float *out;
 };
 int launch_prefill(g4_ctx *ctx, const PrefillArgs &a, hipStream_t stream);
+void release_prefill_plan(g4_ctx *ctx);
 
 int launch_rms_norm_rows(const float *x, int64_t n_rows, int64_t width, const float *w, float eps,
                          float *out, hipStream_t stream);

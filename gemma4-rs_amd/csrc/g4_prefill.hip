@@ -1,29 +1,516 @@
 // Chunked prefill: N queries of one sequence, query i at position pos0 + i,
 // each attending exactly the rows a decode step at that position would
-// (crates/llm-gemma4/src/impl_/generate.rs:37-41, eng/mod.rs:10-36).
+// (crates/llm-gemma4/src/impl_/generate.rs:37-41, eng/mod.rs:10-36): keys
+// [0, p+1) on global layers, [(p+1-W)+, p+1) on sliding-window layers.
+//
+// MFMA tiling (f32, v_mfma_f32_16x16x4f32).  The 8 query heads that share a
+// KV head are folded into the row dimension: a wavefront owns 16 rows (two
+// positions x eight heads) and keeps their Q^T (B operand) and O^T
+// accumulators in registers for the whole key range; a workgroup of four
+// wavefronts covers eight positions and streams 16-key K/V tiles through
+// double-buffered LDS, so every K/V byte fetched is used by 64 query rows.
+// Per tile and wavefront:
+//   S^T[16 keys x 16 rows] = K[16 keys x D] . Q^T[D x 16 rows]     (D/4 MFMAs)
+//   mask (causal / window, per element), online softmax per row
+//   O^T[D x 16 rows]      += V^T[D x 16 keys] . P^T[16 keys x 16 rows] (D/4 MFMAs)
+// Computing S^T leaves lane (g, c) holding keys 4g..4g+3 of row c, which is
+// the B-operand layout P^T needs, so P stays in registers.
+//
+// Work balance: the causal triangle gives the last position blocks many more
+// tiles than the first, so a block's key range is cut into units of at most
+// kPrefillUnitTiles tiles; units are ordered heaviest first.  A block with
+// one unit writes its output directly; otherwise each unit leaves an (m, l, O)
+// partial and a merge kernel combines them in unit order.
+
+#include <algorithm>
+#include <vector>
 
 #include "g4_internal.h"
 
 namespace g4 {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kRowsPerWave = 16;
+constexpr int kWaves = 4;
+constexpr int kPosPerWave = 2;                       // 16 rows = 2 positions x 8 heads
+constexpr int kPosPerBlock = kWaves * kPosPerWave;   // 8
+constexpr int kGroup = 8;                            // query heads per KV head
+constexpr float kRescaleSlack = 8.0f / 1.4426950408889634f;  // 8 in log2 units
+constexpr int kPrefillMaxUnitsDev = 8;  // partial units per block (merge weight table)
+
+struct PrefillUnit {
+    int block;   // position block: positions pos0 + 8*block .. +7
+    int t_lo;    // first 16-key tile
+    int t_hi;    // one past the last tile
+    int slot;    // partial slot, or -1 when the block has a single unit
+};
+
+struct PrefillBlockInfo {
+    int first_slot;
+    int n_units;
+};
+
+struct PrefillK {
+    const float *q;
+    const float *k;
+    const float *v;
+    int64_t row_stride;
+    int64_t pos0, N, window;
+    int n_heads;
+    float scale;
+    float *out;
+    const PrefillUnit *units;
+    const PrefillBlockInfo *blocks;
+    float *part_o;    // [slot][kv head][wave][D/16 tiles][64 lanes] f32x4
+    float2 *part_ml;  // [slot][kv head][64 rows]
+    int n_slots;
+    unsigned *status;
+};
+
+__device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Workgroup geometry for head width D: 4 row groups of 16 rows, each owned by
+// SPLIT wavefronts that divide the head dimension (DH = D / SPLIT dims each),
+// so that one wavefront's Q^T and O^T fit the register file.
+template <int D>
+struct PrefillShape {
+    static constexpr int SPLIT = 2;  // merge grid's z extent is kWaves * SPLIT
+    static constexpr int DH = D / SPLIT;
+    static constexpr int WAVES = kWaves * SPLIT;
+    static constexpr int THREADS = 64 * WAVES;
+};
+
+template <int D>
+__global__ __launch_bounds__(PrefillShape<D>::THREADS, 1) void prefill_kernel(PrefillK p) {
+    using S = PrefillShape<D>;
+    constexpr int DH = S::DH;
+    constexpr int NU = DH / 32;  // 32-dim K chunks per wave
+    constexpr int NV = DH / 64;  // 64-dim V groups per wave
+    constexpr int NT = DH / 16;  // O^T tiles per wave
+    constexpr int TILE_F4 = 16 * D / 4;
+    constexpr int PER_THREAD = TILE_F4 / S::THREADS;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int rg = wave % kWaves, half = wave / kWaves;  // row group, dim half
+    const int g = lane >> 4, c = lane & 15;
+    const int kvh = blockIdx.y;
+    const PrefillUnit u = p.units[blockIdx.x];
+
+    const int64_t P0 = p.pos0 + (int64_t)kPosPerBlock * u.block;
+    const int64_t last_pos = p.pos0 + p.N - 1;
+    const int64_t pos = P0 + kPosPerWave * rg + (c >> 3);  // this lane's row position
+    const bool row_valid = pos <= last_pos;
+    const int head = kvh * kGroup + (c & 7);
+    const int64_t win = p.window;
+    const int d0 = half * DH;  // first dim of this wave
+
+    // One array for both tiles, [buf][0] = K in the swizzle of stage_k,
+    // [buf][1] = V row-major [key][D/4]; the epilogue reuses all of it
+    // (2*2*TILE_F4 float4 = 64*D floats) to transpose the output rows.
+    __shared__ f32x4 lds_kv[2][2][TILE_F4];
+    __shared__ f32x4 lds_s[2][S::WAVES][64];  // partial S^T of the D halves
+
+    // K/V tile loaders: thread tid loads float4 f = tid + THREADS*e of the
+    // tile (row f / (D/4), dims 4*(f % (D/4)) ..).  Rows past the last
+    // position are clamped (masked for every query of the chunk); rows before
+    // the block's first window start are outside every row's attended set and
+    // are staged as zeros, so whatever they hold cannot reach the output
+    // through a zero softmax weight (0 * NaN).  K and V of the next tile are
+    // fetched at different points of the current one, so that only half a
+    // tile is held in registers at a time.
+    const float *kbase = p.k + (int64_t)kvh * D;
+    const float *vbase = p.v + (int64_t)kvh * D;
+    const int64_t block_lo = (win > 0 && P0 + 1 > win) ? P0 + 1 - win : 0;
+    f32x4 rx[PER_THREAD];
+    auto fetch = [&](const float *base, int t) {
+#pragma unroll
+        for (int e = 0; e < PER_THREAD; ++e) {
+            const int f = tid + S::THREADS * e;
+            const int row = f / (D / 4), c4 = f % (D / 4);
+            int64_t key = 16LL * t + row;
+            const bool stale = key < block_lo;
+            if (key > last_pos) key = last_pos;
+            const f32x4 x = *(const f32x4 *)(base + key * p.row_stride + 4 * c4);
+            rx[e] = stale ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : x;
+        }
+    };
+    auto stage_k = [&](int buf) {
+#pragma unroll
+        for (int e = 0; e < PER_THREAD; ++e) {
+            const int f = tid + S::THREADS * e;
+            const int row = f / (D / 4), c4 = f % (D / 4);
+            const int dim = 4 * c4;
+            const int uu = dim >> 5, gg = (dim >> 3) & 3, hh = (dim >> 2) & 1;
+            // The 16 lanes reading one quarter of an MFMA operand read 256
+            // contiguous bytes: index ((u*4 + g)*2 + h)*16 + key.
+            lds_kv[buf][0][((uu * 4 + gg) * 2 + hh) * 16 + row] = rx[e];
+        }
+    };
+    auto stage_v = [&](int buf) {
+#pragma unroll
+        for (int e = 0; e < PER_THREAD; ++e) lds_kv[buf][1][tid + S::THREADS * e] = rx[e];
+    };
+
+    // Q^T (B operand): lane (g, c) holds q[row c][d0 + 32u + 8g + j].
+    float qreg[NU][8];
+    {
+        const int64_t qpos = row_valid ? pos : last_pos;
+        const float *qr = p.q + ((qpos - p.pos0) * p.n_heads + head) * D + d0 + 8 * g;
+#pragma unroll
+        for (int uu = 0; uu < NU; ++uu) {
+            const f32x4 a = *(const f32x4 *)(qr + 32 * uu);
+            const f32x4 b = *(const f32x4 *)(qr + 32 * uu + 4);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                qreg[uu][j] = a[j];
+                qreg[uu][4 + j] = b[j];
+            }
+        }
+    }
+
+    f32x4 o[NT];
+#pragma unroll
+    for (int i = 0; i < NT; ++i) o[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m = -INFINITY, l = 0.0f;
+    bool bad = false;
+
+    fetch(kbase, u.t_lo);
+    stage_k(0);
+    fetch(vbase, u.t_lo);
+    stage_v(0);
+    int buf = 0;
+    for (int t = u.t_lo; t < u.t_hi; ++t) {
+        // The next tile (the current one again on the last step, so that the
+        // loads are unconditional and the compiler's wait counts stay exact).
+        const int tn = t + 1 < u.t_hi ? t + 1 : t;
+        fetch(kbase, tn);  // in flight during this tile's QK^T
+        __syncthreads();   // tile t staged in lds[buf]; buf^1 free
+
+        // Partial S^T over this wave's DH dims: two independent chains.
+        f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int uu = 0; uu < NU; ++uu) {
+            const int ug = d0 / 32 + uu;
+            const f32x4 k0 = lds_kv[buf][0][((ug * 4 + g) * 2 + 0) * 16 + c];
+            const f32x4 k1 = lds_kv[buf][0][((ug * 4 + g) * 2 + 1) * 16 + c];
+            f32x4 &acc = (uu & 1) ? acc1 : acc0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k0[j], qreg[uu][j], acc, 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k1[j], qreg[uu][4 + j], acc, 0, 0, 0);
+        }
+        f32x4 sc = acc0 + acc1;
+        if constexpr (S::SPLIT == 2) {
+            // Full scores = half 0 + half 1, added in that order by both waves.
+            lds_s[buf][wave][lane] = sc;
+            __syncthreads();
+            sc = lds_s[buf][rg][lane] + lds_s[buf][rg + kWaves][lane];
+        }
+        stage_k(buf ^ 1);
+        fetch(vbase, tn);  // in flight during softmax and P.V
+
+        // Exact attended set per row: key <= pos and, with a window, key > pos - W.
+        float sv[4];
+        float mt = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t key = 16LL * t + 4 * g + r;
+            const bool vis = key <= pos && (win == 0 || key > pos - win);
+            const float x = sc[r] * p.scale;
+            bad |= vis && ((x != x) || (x == INFINITY));
+            sv[r] = vis ? x : -INFINITY;
+            mt = fmaxf(mt, sv[r]);
+        }
+        mt = fmaxf(mt, __shfl_xor(mt, 16));
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        // Lazy rescaling: a row keeps its reference max m until a score
+        // exceeds it by more than kRescaleSlack (p <= 2^8 meanwhile, safe in
+        // f32), so O is rescaled a few times per row rather than every tile.
+        if (__any(mt > m + kRescaleSlack)) {
+            const float m_new = fmaxf(m, mt);
+            const float alpha = (m_new == -INFINITY) ? 1.0f : exp2_fast((m - m_new) * kLog2e);
+            l *= alpha;
+            m = m_new;
+#pragma unroll
+            for (int i = 0; i < NT; ++i) o[i] *= alpha;
+        }
+        float pr[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pr[r] = (m == -INFINITY) ? 0.0f : exp2_fast((sv[r] - m) * kLog2e);
+        l += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+
+        // O^T += V^T . P^T over the tile's 16 keys (k-step r: keys 4g + r).
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int U = 0; U < NV; ++U) {
+                const f32x4 vv = lds_kv[buf][1][(4 * g + r) * (D / 4) + d0 / 4 + 16 * U + c];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    o[4 * U + i] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[i], pr[r], o[4 * U + i], 0, 0, 0);
+            }
+
+        stage_v(buf ^ 1);  // buf^1 was last read before this tile's first barrier
+        buf ^= 1;
+    }
+
+    if (__any(bad && row_valid) && lane == 0) atomicOr(p.status, kStatusNonFinite);
+    float lt = l + __shfl_xor(l, 16);
+    lt = lt + __shfl_xor(lt, 32);
+
+    if (u.slot >= 0) {  // partial of a multi-unit block, in the accumulator layout
+        const int64_t sl = (int64_t)u.slot * gridDim.y + kvh;
+        f32x4 *po = (f32x4 *)(p.part_o + sl * (kWaves * kRowsPerWave * D));
+#pragma unroll
+        for (int i = 0; i < NT; ++i) po[(wave * NT + i) * 64 + lane] = o[i];
+        if (g == 0 && half == 0) p.part_ml[sl * (kWaves * kRowsPerWave) + rg * kRowsPerWave + c] = float2{m, lt};
+        return;
+    }
+    // Single unit: normalise and write row-major through LDS (coalesced).
+    __syncthreads();  // every wave is done with the tile buffers
+    static_assert(S::WAVES * kRowsPerWave * DH <= 2 * 2 * TILE_F4 * 4, "transpose fits the tile buffers");
+    float *tr = (float *)&lds_kv[0][0][0] + wave * (kRowsPerWave * DH);
+    const float inv = 1.0f / lt;
+#pragma unroll
+    for (int U = 0; U < NV; ++U)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) tr[c * DH + 64 * U + 4 * (4 * g + r) + i] = o[4 * U + i][r] * inv;
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < kRowsPerWave * DH / 4 / 64; ++e) {
+        const int f = lane + 64 * e;
+        const int row = f / (DH / 4), c4 = f % (DH / 4);
+        const int64_t rpos = P0 + kPosPerWave * rg + (row >> 3);
+        if (rpos > last_pos) continue;
+        float *orow = p.out + ((rpos - p.pos0) * p.n_heads + kvh * kGroup + (row & 7)) * D + d0;
+        *(f32x4 *)(orow + 4 * c4) = *(const f32x4 *)(tr + row * DH + 4 * c4);
+    }
+}
+
+// Combines the units of one position block (and KV head) in unit order for
+// the rows and dims of one producing wavefront (blockIdx.z), then writes
+// them row-major through LDS.  The per-unit loads of an element are
+// unrolled so that they are all in flight together.
+template <int D>
+__global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillK p) {
+    using S = PrefillShape<D>;
+    constexpr int DH = S::DH;
+    constexpr int NT = DH / 16;
+    const PrefillBlockInfo bi = p.blocks[blockIdx.x];
+    if (bi.n_units <= 1) return;
+    const int kvh = blockIdx.y, wave = blockIdx.z;
+    const int rg = wave % kWaves, half = wave / kWaves;
+    const int tid = threadIdx.x;
+    __shared__ float w[kPrefillMaxUnitsDev][kRowsPerWave];
+    __shared__ float Linv[kRowsPerWave];
+    __shared__ float tr[kRowsPerWave * DH];
+    const int n = bi.n_units;
+    if (tid < kRowsPerWave) {
+        const int row = rg * kRowsPerWave + tid;
+        float M = -INFINITY;
+        for (int j = 0; j < n; ++j)
+            M = fmaxf(M, p.part_ml[((int64_t)(bi.first_slot + j) * gridDim.y + kvh) * 64 + row].x);
+        float L = 0.0f;
+        for (int j = 0; j < kPrefillMaxUnitsDev; ++j) {
+            float wj = 0.0f;
+            if (j < n) {
+                const float2 ml = p.part_ml[((int64_t)(bi.first_slot + j) * gridDim.y + kvh) * 64 + row];
+                wj = ml.x == -INFINITY ? 0.0f : exp2_fast((ml.x - M) * kLog2e);
+                L += wj * ml.y;
+            }
+            w[j][tid] = wj;
+        }
+        Linv[tid] = 1.0f / L;
+    }
+    __syncthreads();
+    const int64_t slot_stride = (int64_t)gridDim.y * kWaves * kRowsPerWave * D / 4;  // f32x4
+    const f32x4 *base = (const f32x4 *)p.part_o +
+                        ((int64_t)bi.first_slot * gridDim.y + kvh) * (kWaves * kRowsPerWave * D / 4) +
+                        (int64_t)wave * NT * 64;
+    for (int e = tid; e < NT * 64; e += 256) {
+        const int lane = e & 63, tile = e >> 6;
+        const int g = lane >> 4, c = lane & 15;
+        f32x4 v[kPrefillMaxUnitsDev];
+#pragma unroll
+        for (int j = 0; j < kPrefillMaxUnitsDev; ++j) v[j] = base[(j < n ? j : 0) * slot_stride + e];
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < kPrefillMaxUnitsDev; ++j) acc += w[j][c] * v[j];
+        const int U = tile >> 2, i = tile & 3;
+        const float inv = Linv[c];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) tr[c * DH + 64 * U + 4 * (4 * g + r) + i] = acc[r] * inv;
+    }
+    __syncthreads();
+    const int64_t P0 = p.pos0 + (int64_t)kPosPerBlock * blockIdx.x;
+    const int64_t last_pos = p.pos0 + p.N - 1;
+    for (int f = tid; f < kRowsPerWave * DH / 4; f += 256) {
+        const int row = f / (DH / 4), c4 = f % (DH / 4);
+        const int64_t rpos = P0 + kPosPerWave * rg + (row >> 3);
+        if (rpos <= last_pos) {
+            float *orow = p.out + ((rpos - p.pos0) * p.n_heads + kvh * kGroup + (row & 7)) * D + half * DH;
+            *(f32x4 *)(orow + 4 * c4) = *(const f32x4 *)(tr + row * DH + 4 * c4);
+        }
+    }
+}
+
+constexpr int kPrefillMaxUnits = kPrefillMaxUnitsDev;  // per position block
+
+// Per-context cache of the unit table for the last prefill shape.
+struct PrefillPlan {
+    int64_t pos0 = -1, N = -1, window = -1;
+    int unit_tiles = 0;
+    int n_units = 0, n_blocks = 0, n_slots = 0;
+    PrefillUnit *units = nullptr;
+    PrefillBlockInfo *blocks = nullptr;
+    size_t cap_units = 0, cap_blocks = 0;
+};
+
+}  // namespace
+
+// The plan lives with the context (one per device; prefill calls on one
+// context are issued from one host thread).
+static PrefillPlan &plan_of(g4_ctx *ctx) {
+    if (!ctx->prefill_plan) ctx->prefill_plan = new PrefillPlan();
+    return *static_cast<PrefillPlan *>(ctx->prefill_plan);
+}
+
+void release_prefill_plan(g4_ctx *ctx) {
+    if (!ctx->prefill_plan) return;
+    auto *pl = static_cast<PrefillPlan *>(ctx->prefill_plan);
+    if (pl->units) (void)hipFree(pl->units);
+    if (pl->blocks) (void)hipFree(pl->blocks);
+    delete pl;
+    ctx->prefill_plan = nullptr;
+}
+
+static int build_plan(g4_ctx *ctx, const PrefillArgs &a, PrefillPlan &pl) {
+    // Longest unit: 32 tiles (512 keys) on 512-wide heads, 64 on 256-wide
+    // ones (a 512-key window then needs no merge).
+    const int unit_tiles = a.head_dim > 256 ? 32 : 64;
+    if (pl.pos0 == a.pos0 && pl.N == a.N && pl.window == a.window && pl.unit_tiles == unit_tiles) return G4_OK;
+    const int n_blocks = (int)((a.N + kPosPerBlock - 1) / kPosPerBlock);
+    std::vector<PrefillUnit> units;
+    std::vector<PrefillBlockInfo> blocks(n_blocks);
+    int n_slots = 0;
+    const int64_t last_pos = a.pos0 + a.N - 1;
+    for (int b = 0; b < n_blocks; ++b) {
+        const int64_t P0 = a.pos0 + (int64_t)kPosPerBlock * b;
+        const int64_t P1 = std::min<int64_t>(P0 + kPosPerBlock - 1, last_pos);
+        const int64_t k_lo = (a.window > 0 && P0 + 1 > a.window) ? P0 + 1 - a.window : 0;
+        const int t_lo = (int)(k_lo / 16), t_hi = (int)(P1 / 16 + 1);
+        const int tiles = t_hi - t_lo;
+        const int nu = (tiles + unit_tiles - 1) / unit_tiles;
+        if (nu > kPrefillMaxUnits) return set_error(G4_ERR_COMPUTE, "prefill key range too long for one call");
+        blocks[b] = {nu > 1 ? n_slots : 0, nu};
+        for (int j = 0; j < nu; ++j) {
+            const int lo = t_lo + j * tiles / nu, hi = t_lo + (j + 1) * tiles / nu;
+            units.push_back({b, lo, hi, nu > 1 ? n_slots + j : -1});
+        }
+        if (nu > 1) n_slots += nu;
+    }
+    // Heaviest units first: the hardware dispatches workgroups in order.
+    std::stable_sort(units.begin(), units.end(), [](const PrefillUnit &x, const PrefillUnit &y) {
+        return (x.t_hi - x.t_lo) > (y.t_hi - y.t_lo);
+    });
+    if (units.size() > pl.cap_units) {
+        if (pl.units) G4_HIP(hipFree(pl.units));
+        pl.units = nullptr;
+        G4_HIP(hipMalloc(&pl.units, units.size() * sizeof(PrefillUnit)));
+        pl.cap_units = units.size();
+    }
+    if (blocks.size() > pl.cap_blocks) {
+        if (pl.blocks) G4_HIP(hipFree(pl.blocks));
+        pl.blocks = nullptr;
+        G4_HIP(hipMalloc(&pl.blocks, blocks.size() * sizeof(PrefillBlockInfo)));
+        pl.cap_blocks = blocks.size();
+    }
+    // A new shape uploads its table synchronously (graph capture needs a
+    // previous call with the same shape).
+    G4_HIP(hipMemcpy(pl.units, units.data(), units.size() * sizeof(PrefillUnit), hipMemcpyHostToDevice));
+    G4_HIP(hipMemcpy(pl.blocks, blocks.data(), blocks.size() * sizeof(PrefillBlockInfo), hipMemcpyHostToDevice));
+    pl.pos0 = a.pos0;
+    pl.N = a.N;
+    pl.window = a.window;
+    pl.unit_tiles = unit_tiles;
+    pl.n_units = (int)units.size();
+    pl.n_blocks = n_blocks;
+    pl.n_slots = n_slots;
+    return G4_OK;
+}
 
 int launch_prefill(g4_ctx *ctx, const PrefillArgs &a, hipStream_t stream) {
-    // Every query is an independent decode over its own causal/window range.
-    DecodeArgs d{};
-    d.B = (int)a.N;
-    d.q = a.q;
-    d.k = a.k;
-    d.v = a.v;
-    d.row_stride = a.row_stride;
-    d.pos0 = a.pos0;
-    d.prefill_window = a.window;
-    const int64_t last = a.pos0 + a.N;
-    d.max_kv_len = (a.window > 0 && a.window < last) ? a.window : last;
-    d.n_heads = a.n_heads;
-    d.n_kv_heads = a.n_kv_heads;
-    d.head_dim = a.head_dim;
-    d.scale = a.scale;
-    d.out = a.out;
-    return launch_decode(ctx, d, stream);
+    const int group = a.n_heads / a.n_kv_heads;
+    const bool mfma = (a.head_dim == 256 || a.head_dim == 512) && group == kGroup &&
+                      a.n_heads % a.n_kv_heads == 0;
+    if (!mfma) {
+        // Any other shape: every query as an independent decode over its range.
+        DecodeArgs d{};
+        d.B = (int)a.N;
+        d.q = a.q;
+        d.k = a.k;
+        d.v = a.v;
+        d.row_stride = a.row_stride;
+        d.pos0 = a.pos0;
+        d.prefill_window = a.window;
+        const int64_t last = a.pos0 + a.N;
+        d.max_kv_len = (a.window > 0 && a.window < last) ? a.window : last;
+        d.n_heads = a.n_heads;
+        d.n_kv_heads = a.n_kv_heads;
+        d.head_dim = a.head_dim;
+        d.scale = a.scale;
+        d.out = a.out;
+        return launch_decode(ctx, d, stream);
+    }
+    PrefillPlan &pl = plan_of(ctx);
+    int rc = build_plan(ctx, a, pl);
+    if (rc != G4_OK) return rc;
+    PrefillK p{};
+    p.q = a.q;
+    p.k = a.k;
+    p.v = a.v;
+    p.row_stride = a.row_stride;
+    p.pos0 = a.pos0;
+    p.N = a.N;
+    p.window = a.window;
+    p.n_heads = a.n_heads;
+    p.scale = a.scale;
+    p.out = a.out;
+    p.units = pl.units;
+    p.blocks = pl.blocks;
+    p.n_slots = pl.n_slots;
+    p.status = ctx->status_dev;
+    const int D = a.head_dim;
+    if (pl.n_slots > 0) {
+        const size_t per_slot = (size_t)a.n_kv_heads * kWaves * kRowsPerWave;
+        const size_t obytes = (size_t)pl.n_slots * per_slot * D * sizeof(float);
+        const size_t bytes = obytes + (size_t)pl.n_slots * per_slot * sizeof(float2) + 256;
+        rc = ensure_workspace(ctx, bytes, stream);
+        if (rc != G4_OK) return rc;
+        p.part_o = (float *)ctx->ws.ptr;
+        p.part_ml = (float2 *)((char *)ctx->ws.ptr + (obytes + 255) / 256 * 256);
+    }
+    dim3 grid((unsigned)pl.n_units, (unsigned)a.n_kv_heads);
+    if (D == 256)
+        hipLaunchKernelGGL(prefill_kernel<256>, grid, dim3(PrefillShape<256>::THREADS), 0, stream, p);
+    else
+        hipLaunchKernelGGL(prefill_kernel<512>, grid, dim3(PrefillShape<512>::THREADS), 0, stream, p);
+    G4_HIP(hipGetLastError());
+    if (pl.n_slots > 0) {
+        dim3 mgrid((unsigned)pl.n_blocks, (unsigned)a.n_kv_heads, (unsigned)(kWaves * 2));
+        if (D == 256)
+            hipLaunchKernelGGL(prefill_merge_kernel<256>, mgrid, dim3(256), 0, stream, p);
+        else
+            hipLaunchKernelGGL(prefill_merge_kernel<512>, mgrid, dim3(256), 0, stream, p);
+        G4_HIP(hipGetLastError());
+    }
+    return G4_OK;
 }
 
 }  // namespace g4
