@@ -220,6 +220,33 @@ def bench_ragged(ctx, torch, prep, steps, warmup, B=32, seed=2024):
     return res
 
 
+def bench_copy(torch, steps, nbytes=256 << 20):
+    """A plain device-to-device copy of known size: the reference point that
+    scales the FETCH_SIZE / WRITE_SIZE counters to bytes."""
+    src = torch.empty(nbytes // 4, device="cuda").uniform_()
+    dst = torch.empty_like(src)
+    wall, ev = time_steps(torch, lambda i: dst.copy_(src), steps, 2)
+    return {"bytes_read": nbytes, "bytes_written": nbytes, "us": ev / steps * 1e6,
+            "gbs": 2 * nbytes / (ev / steps) / 1e9}
+
+
+def measured_traffic(profile="decode_global_d512_ctx4096.txt"):
+    """HBM bytes per decode step (split + merge kernels) from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary, or None if it is absent."""
+    path = os.path.join(ROOT, "profiles", profile)
+    if not os.path.exists(path):
+        return None
+    total = 0.0
+    for line in open(path):
+        f = line.split()
+        if len(f) >= 3 and "decode_" in line and "_kernel" in line:
+            try:
+                total += (float(f[-2]) + float(f[-1])) * 1e6
+            except ValueError:
+                continue
+    return int(total) if total else None
+
+
 def cpu_baseline(host, bytes_per_step, seconds):
     """The oracle's attend over the same K/V, with the reference's per-row
     `concat` copy and per-head pool, timed for about `seconds`."""
@@ -252,8 +279,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-workloads", action="store_true", help="only the headline step")
-    ap.add_argument("--only", choices=["global", "sliding", "stack", "prefill", "ragged"],
-                    help="run one workload alone (for profiling); prints its result")
+    ap.add_argument("--only", choices=["global", "sliding", "stack", "prefill", "ragged", "copy"],
+                    help="run one workload alone (for profiling); prints its result.  'copy' is a "
+                         "plain 256 MiB device copy, the reference point for HBM byte counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build runs on a single MI355X (asked for --gpus {args.gpus}).",
@@ -272,7 +300,8 @@ def main():
                   "sliding": lambda: bench_sliding_decode(ctx, torch, prep, args.steps, args.warmup),
                   "stack": lambda: bench_stack(ctx, torch, prep, g4hip, k, 5),
                   "prefill": lambda: bench_prefill(ctx, torch, prep, max(5, k // 10), 2),
-                  "ragged": lambda: bench_ragged(ctx, torch, prep, max(5, k // 4), 2)}[args.only]
+                  "ragged": lambda: bench_ragged(ctx, torch, prep, max(5, k // 4), 2),
+                  "copy": lambda: bench_copy(torch, max(5, k // 4))}[args.only]
             res = fn()
             res.pop("host", None)
             print(json.dumps({"only": args.only, "result": res}))
@@ -313,9 +342,11 @@ def main():
                                "proportional NEOX RoPE inputs", "context": 4096, "head_dim": 512, "n_heads": N_HEADS,
                    "n_kv_heads": N_KV, "kv_copies_rotated": g["copies"], "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "decode split-K + merge (one decode step)",
-                     "bytes_per_launch": g["bytes"]},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "kernel": "decode step: split-K kernel + merge kernel",
+                     "bytes_per_launch": g["bytes"],
+                     "traffic_source": "profiles/decode_global_d512_ctx4096.txt (rocprofv3 --pmc, "
+                                       "scaled by profiles/hbm_counter_calibration.txt)"},
         "cpu_baseline": {"value": round(cpu["pool"]["gbs"], 3), "unit": "GB/s", "cores": threads_used,
                          "kind": "port",
                          "sample": f"{cpu['pool']['calls']} calls of the same step (us/step "
