@@ -38,7 +38,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kDecodeBuffers = 3;  // K/V tiles held per wave (NBUF-1 in flight)
-constexpr int kMaxSplits = 512;  // per (sequence, KV head); bounds the merge's LDS table
+constexpr int kMaxSplits = 512;  // per (sequence, KV head); bounds the split workspace
 
 struct DecodeK {
     const float *q;
@@ -112,6 +112,55 @@ __device__ inline int partial_dim(int e, int G) {
     return w * 64 + 16 * g + i;  // + 4r for component r
 }
 
+// Online-softmax combination of two partials (m, l, o) over disjoint key
+// sets: the result is their union's (max, sum of exp, unnormalised output).
+// Symmetric in its two arguments, bit for bit, so lanes that exchange
+// partials agree.
+__device__ inline void combine_partial(float &m, float &l, f32x4 &o, float m2, float l2, f32x4 o2) {
+    const float mm = fmaxf(m, m2);
+    const float a = (m == -INFINITY) ? 0.0f : exp2_fast((m - mm) * kLog2e);
+    const float b = (m2 == -INFINITY) ? 0.0f : exp2_fast((m2 - mm) * kLog2e);
+    l = a * l + b * l2;
+    o = a * o + b * o2;
+    m = mm;
+}
+
+// Folds a batch of split partials (m_j, l_j) / O_j into the running
+// (m, l, o) of one stored vector; entries at or past n are ignored.
+template <int NB>
+__device__ inline void fold_batch(float &m, float &l, f32x4 &o, const float2 (&t)[NB], const f32x4 (&v)[NB],
+                                  int j0, int jstep, int n) {
+    float mb = m;
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+        if (j0 + jstep * b < n) mb = fmaxf(mb, t[b].x);
+    const float a = (m == -INFINITY) ? 0.0f : exp2_fast((m - mb) * kLog2e);
+    l *= a;
+    o *= a;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const bool use = j0 + jstep * b < n && t[b].x != -INFINITY;
+        const float w = use ? exp2_fast((t[b].x - mb) * kLog2e) : 0.0f;
+        l += w * t[b].y;
+        o += w * v[b];
+    }
+    m = mb;
+}
+
+// Final output of stored vector e (head c = e % G) from its merged partial.
+template <int D>
+__device__ inline void write_merged(const DecodeK &p, int s, int kvh, int e, float m, float l, f32x4 o) {
+    const int G = p.group, c = e % G;
+    if (m == -INFINITY) {  // every score of this head was -inf
+        atomicOr(p.status, kStatusNonFinite);
+        return;
+    }
+    const float inv = 1.0f / l;
+    float *op = p.out + ((int64_t)s * p.n_heads + kvh * G + c) * D + partial_dim(e, G);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) op[4 * r] = o[r] * inv;
+}
+
 // One workgroup = one (split, KV head, sequence); NW wavefronts, each owning
 // 64 of the D = 64*NW head dims.  Tiles of 16 keys are software-pipelined
 // through NBUF register buffers: loads are issued unconditionally (clamped
@@ -132,8 +181,10 @@ __global__ __launch_bounds__(64 * NW, MINB) void decode_split_kernel(DecodeK p) 
             atomicOr(p.status, len <= 0 ? kStatusNonFinite : kStatusRangeTooLong);
         return;
     }
+    // One sequence: the grid is exactly the split count, so no branch here
+    // waits on a kernel argument before the K/V loads are issued.
     const int64_t n_splits = MODE == kSingle ? p.max_splits : num_splits(p, len);
-    if (split >= n_splits) return;
+    if (MODE != kSingle && split >= n_splits) return;
     const int64_t k_lo = begin + ((int64_t)split << p.chunk_shift);
     const int64_t k_hi = (split + 1 == n_splits) ? end : k_lo + (1LL << p.chunk_shift);
 
@@ -290,15 +341,15 @@ __global__ __launch_bounds__(64 * NW, MINB) void decode_split_kernel(DecodeK p) 
 
 // Merges the split partials of one (sequence, KV head):
 // O_c = sum_j e^(m_jc - M_c) O_jc / sum_j e^(m_jc - M_c) l_jc for each head c.
-// A workgroup covers 16 stored vectors x 16 split phases.  Every load it needs
-// -- its partial vectors and the (m, l) table -- is issued before any result
-// is used, so the merge costs about one memory round trip.  Phase sums are
-// added in a fixed order (deterministic).
+// A workgroup covers 16 stored vectors; its 16 thread phases each fold every
+// 16th split into a running partial in registers (all of a batch's loads are
+// issued before any is used), then the phases are combined across lanes and
+// waves in a fixed order (deterministic), and 16 lanes write the result.
 constexpr int kMergeBatch = 16;
-template <int MODE>
-__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeK p, int D) {
+template <int MODE, int D>
+__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeK p) {
     const int s = blockIdx.z, kvh = blockIdx.y;
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     int n = p.max_splits;
     if constexpr (MODE != kSingle) {
         int64_t row0, begin, end;
@@ -307,7 +358,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeK p, int D) {
         if (len <= 0 || len > p.max_kv_len) return;
         n = (int)num_splits(p, len);
     }
-    if (n <= 1) return;
+    if (MODE != kSingle && n <= 1) return;  // kSingle: launched only with splits
     const int G = p.group;
     const int64_t slot0 = ((int64_t)s * p.n_kv_heads + kvh) * p.max_splits;
 
@@ -316,88 +367,40 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeK p, int D) {
     const int c = e % G;
     const f32x4 *src = (const f32x4 *)(p.part_o + slot0 * G * D) + e;
     const int64_t jstride = (int64_t)G * D / 4;
+    const float2 *mlc = p.part_ml + slot0 * G + c;
 
-    __shared__ float2 ml[kMaxSplits * 16];  // (m, l), then (weight, l)
-    __shared__ float red[16][16];
-    __shared__ float Mc[16], Lc[16];
-    __shared__ f32x4 part[16][16];
-
-    // All loads are unconditional (indices clamped into range) so that they
-    // issue back to back: the (m, l) table first, then the partial vectors.
-    const float2 *mlg = p.part_ml + slot0 * G;
-    const int nml = n * G;
-    float2 t[8];
+    float mt = -INFINITY, lt = 0.0f;
+    f32x4 ot = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j0 = ph; j0 < n; j0 += 16 * kMergeBatch) {
+        float2 t[kMergeBatch];
+        f32x4 v[kMergeBatch];
 #pragma unroll
-    for (int b = 0; b < 8; ++b) t[b] = mlg[min(tid + 256 * b, nml - 1)];
-    f32x4 v[kMergeBatch];
-#pragma unroll
-    for (int b = 0; b < kMergeBatch; ++b) v[b] = src[min(ph + 16 * b, n - 1) * jstride];
-#pragma unroll
-    for (int b = 0; b < 8; ++b)
-        if (tid + 256 * b < nml) ml[tid + 256 * b] = t[b];
-    for (int i = tid + 256 * 8; i < nml; i += 256) ml[i] = mlg[i];
-    __syncthreads();
-    // M_c = max_j m_jc: thread (k, cc) scans splits j = k, k+16, ...
-    const int cc = tid & 15, k = tid >> 4;
-    float mx = -INFINITY;
-    if (cc < G)
-        for (int j = k; j < n; j += 16) mx = fmaxf(mx, ml[j * G + cc].x);
-    red[k][cc] = mx;
-    __syncthreads();
-    if (tid < 16) {
-        float mm = red[0][tid];
-        for (int q = 1; q < 16; ++q) mm = fmaxf(mm, red[q][tid]);
-        Mc[tid] = mm;
-    }
-    __syncthreads();
-    float lsum = 0.0f;
-    if (cc < G) {
-        const float M = Mc[cc];
-        for (int j = k; j < n; j += 16) {
-            const float2 t = ml[j * G + cc];
-            const float w = (t.x == -INFINITY) ? 0.0f : exp2_fast((t.x - M) * kLog2e);
-            ml[j * G + cc].x = w;
-            lsum += w * t.y;
-        }
-    }
-    red[k][cc] = lsum;
-    __syncthreads();
-    if (tid < 16) {
-        float ls = red[0][tid];
-        for (int q = 1; q < 16; ++q) ls += red[q][tid];
-        Lc[tid] = ls;
-        if (tid < G && Mc[tid] == -INFINITY && blockIdx.x == 0) atomicOr(p.status, kStatusNonFinite);
-    }
-    __syncthreads();
-
-    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int b = 0; b < kMergeBatch; ++b) {
-        const int j = ph + 16 * b;
-        const float w = ml[min(j, n - 1) * G + c].x;
-        acc += (j < n ? w : 0.0f) * v[b];
-    }
-    for (int j0 = ph + 16 * kMergeBatch; j0 < n; j0 += 16 * kMergeBatch) {
+        for (int b = 0; b < kMergeBatch; ++b) t[b] = mlc[min(j0 + 16 * b, n - 1) * G];
 #pragma unroll
         for (int b = 0; b < kMergeBatch; ++b) v[b] = src[min(j0 + 16 * b, n - 1) * jstride];
-#pragma unroll
-        for (int b = 0; b < kMergeBatch; ++b) {
-            const int j = j0 + 16 * b;
-            const float w = ml[min(j, n - 1) * G + c].x;
-            acc += (j < n ? w : 0.0f) * v[b];
-        }
+        fold_batch(mt, lt, ot, t, v, j0, 16, n);
     }
-    part[ph][el] = acc;
+    // Phases 4w..4w+3 of wave w sit 16 lanes apart.
+#pragma unroll
+    for (int off = 16; off <= 32; off <<= 1) {
+        f32x4 o2;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o2[r] = __shfl_xor(ot[r], off);
+        combine_partial(mt, lt, ot, __shfl_xor(mt, off), __shfl_xor(lt, off), o2);
+    }
+    __shared__ f32x4 red_o[4][16];
+    __shared__ float2 red_ml[4][16];
+    if (lane < 16) {
+        red_o[wave][el] = ot;
+        red_ml[wave][el] = float2{mt, lt};
+    }
     __syncthreads();
-    if (ph == 0) {
-        f32x4 sum = part[0][el];
+    if (tid >= 16) return;
+    float m = red_ml[0][el].x, l = red_ml[0][el].y;
+    f32x4 o = red_o[0][el];
 #pragma unroll
-        for (int q = 1; q < 16; ++q) sum += part[q][el];
-        const float inv = 1.0f / Lc[c];
-        float *op = p.out + ((int64_t)s * p.n_heads + kvh * G + c) * D + partial_dim(e, G);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) op[4 * r] = sum[r] * inv;
-    }
+    for (int w = 1; w < 4; ++w) combine_partial(m, l, o, red_ml[w][el].x, red_ml[w][el].y, red_o[w][el]);
+    write_merged<D>(p, s, kvh, e, m, l, o);
 }
 
 // Any shape the MFMA kernel does not cover (head_dim not a multiple of 256,
@@ -534,8 +537,11 @@ int launch_mode(g4_ctx *ctx, const DecodeArgs &a, DecodeK p, hipStream_t stream)
         hipLaunchKernelGGL((decode_split_kernel<8, MODE, kDecodeBuffers>), grid, dim3(512), 0, stream, p);
     G4_HIP(hipGetLastError());
     if (max_splits > 1) {
-        hipLaunchKernelGGL(decode_merge_kernel<MODE>, dim3(D * group / 64, a.n_kv_heads, a.B), dim3(256), 0,
-                           stream, p, D);
+        const dim3 mgrid(D * group / 64, a.n_kv_heads, a.B);
+        if (D == 256)
+            hipLaunchKernelGGL((decode_merge_kernel<MODE, 256>), mgrid, dim3(256), 0, stream, p);
+        else
+            hipLaunchKernelGGL((decode_merge_kernel<MODE, 512>), mgrid, dim3(256), 0, stream, p);
         G4_HIP(hipGetLastError());
     }
     return G4_OK;
