@@ -14,8 +14,11 @@
 // scores of keys 4g..4g+3 for head c -- exactly the B operand the P.V MFMA
 // needs for k-step r = keys {4g + r}, so P never moves between lanes.
 //
-// A workgroup is D/64 wavefronts that split the head dimension: wave w owns
-// dims [64w, 64w+64) of K, V, q and the output.  Each wave computes a partial
+// A workgroup is 8 wavefronts that split the head dimension: wave w owns
+// dims [DW*w, DW*w + DW) of K, V, q and the output, DW = D/8 (64 for the
+// global layers' D = 512, 32 for the sliding layers' 256: two wavefronts per
+// SIMD either way, so one wave's MFMA chain overlaps the other's softmax and
+// LDS work).  Each wave computes a partial
 // S^T over its dims; the partials are summed through LDS in a fixed order, so
 // every wave sees bit-identical scores and softmax state, then each wave
 // accumulates P.V for its own dims.  Work is split over keys (split-K): a
@@ -34,11 +37,19 @@
 namespace g4 {
 namespace {
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kDecodeBuffers = 3;  // K/V tiles held per wave (NBUF-1 in flight)
+constexpr int kDecodeBuffers = 4;  // K/V tiles held per wave: a pair computed, a pair in flight
 constexpr int kMaxSplits = 512;  // per (sequence, KV head); bounds the split workspace
+// Wavefronts per split workgroup for head dim D.
+constexpr int decode_waves(int D) { return D == 512 ? 8 : 8; }
+// The online softmax keeps a reference maximum m and moves it only when a
+// score exceeds it by more than this (natural-log units; p <= 2^8 meanwhile,
+// safe in f32), so the accumulators are rescaled a few times per split, not
+// per tile.
+constexpr float kRescaleSlack = 8.0f / 1.4426950408889634f;
 
 struct DecodeK {
     const float *q;
@@ -95,21 +106,58 @@ __device__ inline int64_t num_splits(const DecodeK &p, int64_t len) {
 
 __device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Per-wave geometry for head dim D (256 or 512): DW dims per wave, KU
+// 16-dim groups of S^T steps, TW O^T tiles of 16 rows (one dim per lane and
+// tile of a V row).
+template <int D>
+struct DecodeShape {
+    static constexpr int NW = decode_waves(D);
+    static constexpr int DW = D / NW;   // 32 or 64
+    static constexpr int KU = DW / 16;  // 2 or 4
+    static constexpr int TW = DW / 16;  // 2 or 4
+};
+
+template <int N> struct FloatVec;
+template <> struct FloatVec<2> { typedef f32x2 type; };
+template <> struct FloatVec<4> { typedef f32x4 type; };
+
 // One 16-key tile of K and V in registers, in the MFMA operand layouts of
-// lane (g, c): K rows t0 + c, dims base + 32u + 8g .. +7 (A of S^T = K.Q^T);
-// V rows t0 + 4g + r, dims base + 4c .. +3 (A of O^T = V^T.P^T).
+// lane (g, c) of a wave owning dims [base, base + DW):
+//   k[u] = K[t0 + c][base + 16u + 4g .. +3]  (A of S^T = K.Q^T, steps 4u..4u+3;
+//          the 4 lanes of a key read 64 contiguous bytes)
+//   v[r] = V[t0 + 4g + r][base + TW*c .. +TW-1]  (A of O^T = V^T.P^T, one dim per O^T tile)
+template <int D>
 struct KvTile {
-    f32x4 k[2][2];
-    f32x4 v[4];
+    f32x4 k[DecodeShape<D>::KU];
+    typename FloatVec<DecodeShape<D>::TW>::type v[4];
 };
 
 // Split partials are stored in the accumulator layout, so every lane writes
-// whole 16-byte vectors: for wave w, output tile i, lane group g and head c,
-// the four rows r of O^T (dims w*64 + 16g + 4r + i) are one f32x4 at
-// element ((w*4 + i)*4 + g)*G + c of the split's D*G/4 vectors.
-__device__ inline int partial_dim(int e, int G) {
-    const int g = (e / G) & 3, i = (e / (4 * G)) & 3, w = e / (16 * G);
-    return w * 64 + 16 * g + i;  // + 4r for component r
+// whole 16-byte vectors: for wave w, O^T tile i, lane group g and head c, the
+// four rows r (dims w*DW + TW*(4g + r) + i) are one f32x4 at element
+// ((w*TW + i)*4 + g)*G + c of the split's D*G/4 vectors.  Returns the dim of
+// component 0; component r is TW*r further.
+template <int D>
+__device__ inline int partial_dim0(int e, int G) {
+    constexpr int DW = DecodeShape<D>::DW, TW = DecodeShape<D>::TW;
+    const int g = (e / G) & 3, wi = e / (4 * G);
+    return (wi / TW) * DW + 4 * TW * g + wi % TW;
+}
+
+// Reductions over the four 16-lane rows of a wavefront (lanes c, c+16,
+// c+32, c+48), done with row swaps on the VALU -- no LDS round trip -- and
+// identical in every lane: rows (0,1) and (2,3) first, then the halves.
+__device__ inline float rows_max(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    const float h = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(h), __float_as_uint(h), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ inline float rows_sum(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    const float h = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(h), __float_as_uint(h), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 // Online-softmax combination of two partials (m, l, o) over disjoint key
@@ -156,20 +204,32 @@ __device__ inline void write_merged(const DecodeK &p, int s, int kvh, int e, flo
         return;
     }
     const float inv = 1.0f / l;
-    float *op = p.out + ((int64_t)s * p.n_heads + kvh * G + c) * D + partial_dim(e, G);
+    float *op = p.out + ((int64_t)s * p.n_heads + kvh * G + c) * D + partial_dim0<D>(e, G);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) op[4 * r] = o[r] * inv;
+    for (int r = 0; r < 4; ++r) op[DecodeShape<D>::TW * r] = o[r] * inv;
 }
 
+// Buffer resource (V#) word 3 for raw 32-bit-element buffers on gfx9-class
+// GPUs, gfx950 included.
+constexpr int kBufferWord3 = 0x00020000;
+
 // One workgroup = one (split, KV head, sequence); NW wavefronts, each owning
-// 64 of the D = 64*NW head dims.  Tiles of 16 keys are software-pipelined
-// through NBUF register buffers: loads are issued unconditionally (clamped
-// rows), so the compiler's wait counts stay exact and never wait on a
-// prefetch.
-template <int NW, int MODE, int NBUF, int MINB = 1>
-__global__ __launch_bounds__(64 * NW, MINB) void decode_split_kernel(DecodeK p) {
-    constexpr int D = 64 * NW;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// DW = D/NW of the head dims.  Tiles of 16 keys are software-pipelined
+// through NBUF register buffers.  K and V are read through buffer resources
+// spanning exactly this split's rows: a load is the resource + a per-lane
+// byte offset fixed for the whole split + the tile's offset (one add), and
+// rows past the split's end read as zeros in hardware (their scores are
+// masked, and zero V keeps 0 * V finite).  Loads
+// are issued unconditionally, so the compiler's wait counts stay exact and
+// never wait on a prefetch.
+template <int D, int MODE, int NBUF>
+__global__ __launch_bounds__(64 * DecodeShape<D>::NW) void decode_split_kernel(DecodeK p) {
+    using Shape = DecodeShape<D>;
+    constexpr int NW = Shape::NW, DW = Shape::DW, KU = Shape::KU, TW = Shape::TW;
+    typedef typename FloatVec<TW>::type VRow;
+    // The wave index is uniform across a wavefront; saying so keeps the
+    // buffer resources and tile offsets in scalar registers.
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, c = lane & 15;
     const int split = blockIdx.x, kvh = blockIdx.y, s = blockIdx.z;
 
@@ -187,138 +247,174 @@ __global__ __launch_bounds__(64 * NW, MINB) void decode_split_kernel(DecodeK p) 
     if (MODE != kSingle && split >= n_splits) return;
     const int64_t k_lo = begin + ((int64_t)split << p.chunk_shift);
     const int64_t k_hi = (split + 1 == n_splits) ? end : k_lo + (1LL << p.chunk_shift);
+    const int n_keys = (int)(k_hi - k_lo);
+    const int n_tiles = (n_keys + 15) >> 4;
 
-    const int base = wave * 64;
+    const int base = wave * DW;
     const bool col_valid = c < p.group;
     const int head = kvh * p.group + (col_valid ? c : 0);
-    const float *kcol = p.k + row0 * p.row_stride + (int64_t)kvh * D + base + 8 * g;
-    const float *vcol = p.v + row0 * p.row_stride + (int64_t)kvh * D + base + 4 * c;
-    const int stride = (int)p.row_stride;  // fits: checked by the launcher
-
-    // Rows past k_hi are clamped to k_hi - 1 (loaded, then masked).
-    auto load_tile = [&](int64_t t0, KvTile &T) {
-        const int last = (int)(k_hi - 1 - t0);
-        const float *kt = kcol + t0 * p.row_stride;
-        const float *kp = kt + (c < last ? c : last) * stride;
+    const int stride = (int)p.row_stride;  // 16 rows of it fit 32-bit byte offsets (checked by the launcher)
+    const float *kbase = p.k + (row0 + k_lo) * p.row_stride + (int64_t)kvh * D + base;
+    const float *vbase = p.v + (row0 + k_lo) * p.row_stride + (int64_t)kvh * D + base;
+    // The split's rows span < 2^31 bytes (checked by the launcher).
+    const int records = (n_keys - 1) * stride * 4 + DW * 4;
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc((void *)kbase, 0, records, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc((void *)vbase, 0, records, kBufferWord3);
+    const uint32_t tile_bytes = 64u * (uint32_t)stride;
+    // Lane (g, c) reads K row c (dims 16u + 4g..+3) and V rows 4g + r (dims
+    // TW*c..+TW-1) of a tile.
+    const uint32_t koff = (uint32_t)(c * stride + 4 * g) * 4u;
+    uint32_t voff[4];
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            T.k[u][0] = *(const f32x4 *)(kp + 32 * u);
-            T.k[u][1] = *(const f32x4 *)(kp + 32 * u + 4);
-        }
-        const float *vt = vcol + t0 * p.row_stride;
+    for (int r = 0; r < 4; ++r) voff[r] = (uint32_t)((4 * g + r) * stride + TW * c) * 4u;
+    // The tile offset goes into the per-lane offset: the hardware range
+    // check covers that offset (not the scalar one), so every row at or past
+    // the split's end -- in the last tile, or a whole tile past it -- reads 0.
+    auto load_tile = [&](int tile, KvTile<D> &T) {
+        const uint32_t toff = (uint32_t)tile * tile_bytes;
+#pragma unroll
+        for (int u = 0; u < KU; ++u)
+            T.k[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, koff + toff + 64u * u, 0, 0));
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int rv = 4 * g + r;
-            T.v[r] = *(const f32x4 *)(vt + (rv < last ? rv : last) * stride);
+            if constexpr (TW == 4)
+                T.v[r] = __builtin_bit_cast(VRow, __builtin_amdgcn_raw_buffer_load_b128(vrs, voff[r] + toff, 0, 0));
+            else
+                T.v[r] = __builtin_bit_cast(VRow, __builtin_amdgcn_raw_buffer_load_b64(vrs, voff[r] + toff, 0, 0));
         }
     };
 
-    // Ring of NBUF tiles: NBUF-1 tiles are in flight while one is computed.
-    const int n_tiles = (int)((k_hi - k_lo + 15) >> 4);
-    KvTile T[NBUF];
+    // Tiles are processed in pairs (32 keys): the two score chains, the
+    // cross-wave sum, the softmax bookkeeping and the P.V chains of a pair
+    // run together, so each fixed latency -- the barrier, the LDS round trip,
+    // the softmax's dependent steps -- is paid once per 32 keys.  A pair's
+    // second tile past the end (odd tile count) reads zeros and is masked.
+    // Pairs stream through NPAIR register slots, NPAIR-1 pairs in flight.
+    constexpr int NPAIR = NBUF / 2;
+    const int n_pairs = (n_tiles + 1) >> 1;
+    KvTile<D> T[NPAIR][2];
+    auto load_pair = [&](int q, KvTile<D> (&P)[2]) {
+        load_tile(2 * q, P[0]);
+        load_tile(2 * q + 1, P[1]);
+    };
 #pragma unroll
-    for (int b = 0; b < NBUF - 1; ++b) load_tile(k_lo + 16 * (b < n_tiles ? b : n_tiles - 1), T[b]);
+    for (int b = 0; b < NPAIR - 1; ++b) load_pair(b < n_pairs ? b : n_pairs - 1, T[b]);
 
-    // Q^T as the B operand: lane (g, c) holds q[head c][base + 32u + 8g + j].
-    float qreg[2][8];
+    // Q^T as the B operand: lane (g, c) holds q[head c][base + 16u + 4g + j].
+    float qreg[KU][4];
     {
-        const float *qh = p.q + ((int64_t)s * p.n_heads + head) * D + base + 8 * g;
+        const float *qh = p.q + ((int64_t)s * p.n_heads + head) * D + base + 4 * g;
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const f32x4 a = *(const f32x4 *)(qh + 32 * u);
-            const f32x4 b = *(const f32x4 *)(qh + 32 * u + 4);
+        for (int u = 0; u < KU; ++u) {
+            const f32x4 a = *(const f32x4 *)(qh + 16 * u);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                qreg[u][j] = col_valid ? a[j] : 0.0f;
-                qreg[u][4 + j] = col_valid ? b[j] : 0.0f;
-            }
+            for (int j = 0; j < 4; ++j) qreg[u][j] = col_valid ? a[j] : 0.0f;
         }
     }
 
-    __shared__ f32x4 sx[2][NW][64];  // partial S^T exchange, double-buffered
+    __shared__ f32x4 sx[2][2][NW][64];  // partial S^T of a pair, double-buffered
 
-    float m = -INFINITY, l = 0.0f;
+    float m = -INFINITY, l = 0.0f;  // reference maximum, sum of exp relative to it
     bool bad = false;
-    f32x4 o[4];
+    f32x4 o[TW];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) o[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = 0; i < TW; ++i) o[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     int buf = 0;
 
-    auto compute_tile = [&](int64_t t0, const KvTile &T) {
-        // Partial S^T over this wave's 64 dims, two independent MFMA chains.
-        f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto compute_pair = [&](int q, const KvTile<D> (&P)[2]) {
+        // Partial S^T of both tiles over this wave's dims (two MFMA chains).
+        f32x4 acc[2] = {};
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(T.k[0][j >> 2][j & 3], qreg[0][j], acc0, 0, 0, 0);
-            acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(T.k[1][j >> 2][j & 3], qreg[1][j], acc1, 0, 0, 0);
-        }
-        sx[buf][wave][lane] = acc0 + acc1;
+        for (int u = 0; u < KU; ++u)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(P[t].k[u][j], qreg[u][j], acc[t], 0, 0, 0);
+
+        // The tiles' S^T: the waves' partials summed in a fixed order, so
+        // every wave holds the same bits (all reads issue before the first add).
+        sx[buf][0][wave][lane] = acc[0];
+        sx[buf][1][wave][lane] = acc[1];
         __syncthreads();
-        f32x4 sc = sx[buf][0][lane];
+        f32x4 sc[2];
 #pragma unroll
-        for (int w = 1; w < NW; ++w) sc += sx[buf][w][lane];
+        for (int t = 0; t < 2; ++t) {
+            f32x4 v[NW];
+#pragma unroll
+            for (int w = 0; w < NW; ++w) v[w] = sx[buf][t][w][lane];
+            if constexpr (NW == 8)
+                sc[t] = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+            else
+                sc[t] = (v[0] + v[1]) + (v[2] + v[3]);
+        }
         buf ^= 1;
 
-        // Scores of keys t0 + 4g + r for head c; mask the tail.
-        float sv[4];
-        float mt = -INFINITY;
-        const int64_t valid = k_hi - t0;
+        // Scores of keys 16t + 4g + r of the pair for head c; NaN or +inf
+        // fails the call; keys past the end (last pair only) are masked.
+        float sv[8];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const float x = sc[r] * p.scale;
-            bad |= (x != x) || (x == INFINITY);
-            sv[r] = (4 * g + r < valid) ? x : -INFINITY;
-            mt = fmaxf(mt, sv[r]);
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                sv[4 * t + r] = sc[t][r] * p.scale;
+                bad |= __builtin_amdgcn_classf(sv[4 * t + r], 0x203);  // signalling/quiet NaN, +inf
+            }
+        const int valid = n_keys - 32 * q;
+        if (valid < 32) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                if (16 * (k >> 2) + 4 * g + (k & 3) >= valid) sv[k] = -INFINITY;
         }
-        mt = fmaxf(mt, __shfl_xor(mt, 16));
-        mt = fmaxf(mt, __shfl_xor(mt, 32));
-        const float m_new = fmaxf(m, mt);
-        float alpha, pr[4];
-        if (m_new == -INFINITY) {  // every score so far is -inf: nothing accumulates
-            alpha = 1.0f;
+        const float mt = rows_max(fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
+                                        fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7]))));
+        // Move the reference maximum only when a score outgrows it.
+        const bool grow = mt > m + kRescaleSlack;
+        if (__any(grow)) {
+            const float m_new = grow ? mt : m;
+            const float alpha = grow ? exp2_fast((m - m_new) * kLog2e) : 1.0f;
+            l *= alpha;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) pr[r] = 0.0f;
-        } else {
-            alpha = exp2_fast((m - m_new) * kLog2e);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) pr[r] = exp2_fast((sv[r] - m_new) * kLog2e);
+            for (int i = 0; i < TW; ++i) o[i] *= alpha;
+            m = m_new;
         }
-        l = l * alpha + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
-        m = m_new;
+        float pr[8];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) o[i] *= alpha;
+        for (int k = 0; k < 8; ++k) pr[k] = (m == -INFINITY) ? 0.0f : exp2_fast((sv[k] - m) * kLog2e);
+        l += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
 
-        // O^T += V^T . P^T; k-step r covers keys {t0 + 4g + r}; tile i holds
-        // dims base + 4c' + i for output row c'.
+        // O^T += V^T . P^T: k-step (t, r) covers key 16t + 4g + r; O^T tile i
+        // holds dims base + TW*c' + i for output row c'.
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                o[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(T.v[r][i], pr[r], o[i], 0, 0, 0);
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int i = 0; i < TW; ++i)
+                    o[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(P[t].v[r][i], pr[4 * t + r], o[i], 0, 0, 0);
     };
 
-    // Steady state: each step issues the load of the tile NBUF-1 ahead
+    // Steady state: each step issues the loads of the pair NPAIR-1 ahead
     // (clamped into range, so every load is unconditional and the wait
-    // counts stay exact), then computes the oldest buffered tile.
-    int i = 0;
-    for (; i + NBUF - 1 < n_tiles; i += NBUF) {
+    // counts stay exact), then computes the oldest buffered pair.
+    int q0 = 0;
+    for (; q0 + NPAIR - 1 < n_pairs; q0 += NPAIR) {
 #pragma unroll
-        for (int b = 0; b < NBUF; ++b) {
-            const int pf = i + b + NBUF - 1;
-            load_tile(k_lo + 16 * (pf < n_tiles ? pf : n_tiles - 1), T[(b + NBUF - 1) % NBUF]);
-            compute_tile(k_lo + 16 * (i + b), T[b]);
+        for (int b = 0; b < NPAIR; ++b) {
+            const int pf = q0 + b + NPAIR - 1;
+            load_pair(pf < n_pairs ? pf : n_pairs - 1, T[(b + NPAIR - 1) % NPAIR]);
+            compute_pair(q0 + b, T[b]);
         }
     }
-    // Tail: the remaining (< NBUF) tiles are already buffered in T[0..].
+    // Tail: the remaining (< NPAIR) pairs are already buffered in T[0..].
 #pragma unroll
-    for (int b = 0; b < NBUF - 1; ++b)
-        if (i + b < n_tiles) compute_tile(k_lo + 16 * (i + b), T[b]);
+    for (int b = 0; b < NPAIR - 1; ++b)
+        if (q0 + b < n_pairs) compute_pair(q0 + b, T[b]);
 
     if (wave == 0 && __any(bad && col_valid) && lane == 0) atomicOr(p.status, kStatusNonFinite);
 
     // Sum of exp over the split for head c (lanes c, c+16, c+32, c+48).
-    float lt = l + __shfl_xor(l, 16);
-    lt = lt + __shfl_xor(lt, 32);
+    const float lt = rows_sum(l);
 
     if (n_splits == 1) {
         if (m == -INFINITY && wave == 0 && lane == 0) atomicOr(p.status, kStatusNonFinite);
@@ -326,16 +422,16 @@ __global__ __launch_bounds__(64 * NW, MINB) void decode_split_kernel(DecodeK p) 
         const float inv = 1.0f / lt;
         float *op = p.out + ((int64_t)s * p.n_heads + head) * D + base;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < TW; ++i)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) op[4 * (4 * g + r) + i] = o[i][r] * inv;
+            for (int r = 0; r < 4; ++r) op[TW * (4 * g + r) + i] = o[i][r] * inv;
         return;
     }
     if (!col_valid) return;
     const int64_t slot = ((int64_t)s * p.n_kv_heads + kvh) * p.max_splits + split;
     f32x4 *po = (f32x4 *)(p.part_o + slot * p.group * D);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) po[((wave * 4 + i) * 4 + g) * p.group + c] = o[i];
+    for (int i = 0; i < TW; ++i) po[((wave * TW + i) * 4 + g) * p.group + c] = o[i];
     if (wave == 0 && g == 0) p.part_ml[slot * p.group + c] = float2{m, lt};
 }
 
@@ -487,7 +583,7 @@ int launch_mode(g4_ctx *ctx, const DecodeArgs &a, DecodeK p, hipStream_t stream)
     const int D = a.head_dim;
     const int group = p.group;
     const bool mfma = (D == 256 || D == 512) && group <= 16 && a.n_heads % a.n_kv_heads == 0 &&
-                      a.row_stride <= (1LL << 26);  // 16 rows of stride fit 32-bit offsets
+                      a.row_stride <= (1LL << 25);  // 16 rows of stride fit 32-bit byte offsets
     if (!mfma) {
         if (D > 1024) return set_error(G4_ERR_COMPUTE, "head_dim above 1024 is not supported");
         p.chunk_shift = 62;
@@ -516,6 +612,11 @@ int launch_mode(g4_ctx *ctx, const DecodeArgs &a, DecodeK p, hipStream_t stream)
     }
     const int64_t min_chunk = (max_len + kMaxSplits - 1) / kMaxSplits;
     if (chunk < min_chunk) chunk = min_chunk;
+    // The kernel addresses a split's rows with 32-bit byte offsets.
+    const int64_t max_chunk = (1LL << 31) / (a.row_stride * (int64_t)sizeof(float)) / 2;
+    if (chunk > max_chunk) chunk = max_chunk;
+    if (chunk < min_chunk || max_chunk < 16)
+        return set_error(G4_ERR_COMPUTE, "K/V range too large for the decode kernel's addressing");
     int shift = 4;
     while ((1LL << shift) < chunk) ++shift;
     const int64_t max_splits = (max_len + (1LL << shift) - 1) >> shift;
@@ -532,9 +633,11 @@ int launch_mode(g4_ctx *ctx, const DecodeArgs &a, DecodeK p, hipStream_t stream)
     }
     dim3 grid((unsigned)max_splits, (unsigned)a.n_kv_heads, (unsigned)a.B);
     if (D == 256)
-        hipLaunchKernelGGL((decode_split_kernel<4, MODE, kDecodeBuffers>), grid, dim3(256), 0, stream, p);
+        hipLaunchKernelGGL((decode_split_kernel<256, MODE, kDecodeBuffers>), grid,
+                           dim3(64 * DecodeShape<256>::NW), 0, stream, p);
     else
-        hipLaunchKernelGGL((decode_split_kernel<8, MODE, kDecodeBuffers>), grid, dim3(512), 0, stream, p);
+        hipLaunchKernelGGL((decode_split_kernel<512, MODE, kDecodeBuffers>), grid,
+                           dim3(64 * DecodeShape<512>::NW), 0, stream, p);
     G4_HIP(hipGetLastError());
     if (max_splits > 1) {
         const dim3 mgrid(D * group / 64, a.n_kv_heads, a.B);
