@@ -69,6 +69,8 @@ struct DecodeK {
     float *part_o;   // per (sequence, KV head, split): D*G floats, accumulator layout
     float2 *part_ml; // [B][n_kv][max_splits][group]  (running max, sum of exp)
     unsigned *status;
+    int n_seqs;      // B
+    int *plan;       // streamed batches: pair prefix sums [B+1], then pairs per workgroup
 };
 
 // How a launch names each sequence's rows.  The form is a template parameter
@@ -77,7 +79,8 @@ struct DecodeK {
 enum Mode : int {
     kSingle = 0,  // one sequence: rows [kv_begin0, kv_end0)
     kBatch = 1,   // B sequences: rows [kv_begin[s], kv_end[s]) of a cache starting at row seq_row0[s]
-    kPrefill = 2  // N queries of one sequence at positions pos0 + s (causal / windowed)
+    kPrefill = 2, // N queries of one sequence at positions pos0 + s (causal / windowed)
+    kStream = 3   // kBatch rows through decode_stream_kernel (merge only)
 };
 
 // Rows [begin, end) that sequence s attends, and where its cache starts.
@@ -213,64 +216,49 @@ __device__ inline void write_merged(const DecodeK &p, int s, int kvh, int e, flo
 // GPUs, gfx950 included.
 constexpr int kBufferWord3 = 0x00020000;
 
-// One workgroup = one (split, KV head, sequence); NW wavefronts, each owning
-// DW = D/NW of the head dims.  Tiles of 16 keys are software-pipelined
-// through NBUF register buffers.  K and V are read through buffer resources
-// spanning exactly this split's rows: a load is the resource + a per-lane
-// byte offset fixed for the whole split + the tile's offset (one add), and
-// rows past the split's end read as zeros in hardware (their scores are
-// masked, and zero V keeps 0 * V finite).  Loads
-// are issued unconditionally, so the compiler's wait counts stay exact and
-// never wait on a prefetch.
-template <int D, int MODE, int NBUF>
-__global__ __launch_bounds__(64 * DecodeShape<D>::NW) void decode_split_kernel(DecodeK p) {
+// A wavefront's view of one (sequence, KV head) decode: lane (g, c) =
+// (lane/16, lane%16) of wave w, which owns head dims [base, base + DW).
+// K and V are read through buffer resources spanning exactly the rows being
+// attended: a load is the resource + a per-lane byte offset fixed for the
+// call + the tile's offset (one add), and rows past the end read as zeros in
+// hardware (their scores are masked, and zero V keeps 0 * V finite).
+template <int D>
+struct DecodeLane {
     using Shape = DecodeShape<D>;
-    constexpr int NW = Shape::NW, DW = Shape::DW, KU = Shape::KU, TW = Shape::TW;
+    static constexpr int NW = Shape::NW, DW = Shape::DW, KU = Shape::KU, TW = Shape::TW;
     typedef typename FloatVec<TW>::type VRow;
-    // The wave index is uniform across a wavefront; saying so keeps the
-    // buffer resources and tile offsets in scalar registers.
-    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int g = lane >> 4, c = lane & 15;
-    const int split = blockIdx.x, kvh = blockIdx.y, s = blockIdx.z;
+    int lane, wave, g, c, base;
+    uint32_t koff, voff[4], tile_bytes;
 
-    int64_t row0, begin, end;
-    seq_range<MODE>(p, s, row0, begin, end);
-    const int64_t len = end - begin;
-    if (MODE != kSingle && (len <= 0 || len > p.max_kv_len)) {  // kSingle: checked by the host
-        if (split == 0 && kvh == 0 && threadIdx.x == 0)
-            atomicOr(p.status, len <= 0 ? kStatusNonFinite : kStatusRangeTooLong);
-        return;
-    }
-    // One sequence: the grid is exactly the split count, so no branch here
-    // waits on a kernel argument before the K/V loads are issued.
-    const int64_t n_splits = MODE == kSingle ? p.max_splits : num_splits(p, len);
-    if (MODE != kSingle && split >= n_splits) return;
-    const int64_t k_lo = begin + ((int64_t)split << p.chunk_shift);
-    const int64_t k_hi = (split + 1 == n_splits) ? end : k_lo + (1LL << p.chunk_shift);
-    const int n_keys = (int)(k_hi - k_lo);
-    const int n_tiles = (n_keys + 15) >> 4;
-
-    const int base = wave * DW;
-    const bool col_valid = c < p.group;
-    const int head = kvh * p.group + (col_valid ? c : 0);
-    const int stride = (int)p.row_stride;  // 16 rows of it fit 32-bit byte offsets (checked by the launcher)
-    const float *kbase = p.k + (row0 + k_lo) * p.row_stride + (int64_t)kvh * D + base;
-    const float *vbase = p.v + (row0 + k_lo) * p.row_stride + (int64_t)kvh * D + base;
-    // The split's rows span < 2^31 bytes (checked by the launcher).
-    const int records = (n_keys - 1) * stride * 4 + DW * 4;
-    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc((void *)kbase, 0, records, kBufferWord3);
-    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc((void *)vbase, 0, records, kBufferWord3);
-    const uint32_t tile_bytes = 64u * (uint32_t)stride;
-    // Lane (g, c) reads K row c (dims 16u + 4g..+3) and V rows 4g + r (dims
-    // TW*c..+TW-1) of a tile.
-    const uint32_t koff = (uint32_t)(c * stride + 4 * g) * 4u;
-    uint32_t voff[4];
+    __device__ __forceinline__ explicit DecodeLane(int stride) {
+        lane = threadIdx.x & 63;
+        // The wave index is uniform across a wavefront; saying so keeps the
+        // buffer resources and tile offsets in scalar registers.
+        wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        g = lane >> 4;
+        c = lane & 15;
+        base = wave * DW;
+        tile_bytes = 64u * (uint32_t)stride;
+        // Lane (g, c) reads K row c (dims 16u + 4g..+3) and V rows 4g + r
+        // (dims TW*c..+TW-1) of a tile.  16 rows of stride fit 32 bits
+        // (checked by the launcher).
+        koff = (uint32_t)(c * stride + 4 * g) * 4u;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) voff[r] = (uint32_t)((4 * g + r) * stride + TW * c) * 4u;
+        for (int r = 0; r < 4; ++r) voff[r] = (uint32_t)((4 * g + r) * stride + TW * c) * 4u;
+    }
+
+    // Resource over n_keys rows starting at `first_row` (this wave's dims);
+    // the rows span < 2^31 bytes (checked by the launcher).
+    __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows(const float *first_row, int n_keys, int stride) const {
+        const int records = (n_keys - 1) * stride * 4 + DW * 4;
+        return __builtin_amdgcn_make_buffer_rsrc((void *)(first_row + base), 0, records, kBufferWord3);
+    }
+
     // The tile offset goes into the per-lane offset: the hardware range
     // check covers that offset (not the scalar one), so every row at or past
-    // the split's end -- in the last tile, or a whole tile past it -- reads 0.
-    auto load_tile = [&](int tile, KvTile<D> &T) {
+    // the end -- in the last tile, or a whole tile past it -- reads 0.
+    __device__ __forceinline__ void load_tile(__amdgpu_buffer_rsrc_t krs, __amdgpu_buffer_rsrc_t vrs, int tile,
+                                              KvTile<D> &T) const {
         const uint32_t toff = (uint32_t)tile * tile_bytes;
 #pragma unroll
         for (int u = 0; u < KU; ++u)
@@ -282,46 +270,46 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::NW) void decode_split_kernel(D
             else
                 T.v[r] = __builtin_bit_cast(VRow, __builtin_amdgcn_raw_buffer_load_b64(vrs, voff[r] + toff, 0, 0));
         }
-    };
+    }
+};
 
-    // Tiles are processed in pairs (32 keys): the two score chains, the
-    // cross-wave sum, the softmax bookkeeping and the P.V chains of a pair
-    // run together, so each fixed latency -- the barrier, the LDS round trip,
-    // the softmax's dependent steps -- is paid once per 32 keys.  A pair's
-    // second tile past the end (odd tile count) reads zeros and is masked.
-    // Pairs stream through NPAIR register slots, NPAIR-1 pairs in flight.
-    constexpr int NPAIR = NBUF / 2;
-    const int n_pairs = (n_tiles + 1) >> 1;
-    KvTile<D> T[NPAIR][2];
-    auto load_pair = [&](int q, KvTile<D> (&P)[2]) {
-        load_tile(2 * q, P[0]);
-        load_tile(2 * q + 1, P[1]);
-    };
-#pragma unroll
-    for (int b = 0; b < NPAIR - 1; ++b) load_pair(b < n_pairs ? b : n_pairs - 1, T[b]);
+// Partial S^T of a pair, double-buffered: [buffer][tile][wave][lane].
+template <int D>
+using PairScores = f32x4[2][2][DecodeShape<D>::NW][64];
 
-    // Q^T as the B operand: lane (g, c) holds q[head c][base + 16u + 4g + j].
+// Online-softmax state of one wave for one (sequence, KV head): Q^T as the
+// B operand (lane (g, c) holds q[head c][base + 16u + 4g + j]), the
+// reference maximum m and sum of exp l of head c, and this wave's O^T tiles.
+template <int D>
+struct DecodeAcc {
+    using L = DecodeLane<D>;
+    static constexpr int NW = L::NW, KU = L::KU, TW = L::TW;
     float qreg[KU][4];
-    {
-        const float *qh = p.q + ((int64_t)s * p.n_heads + head) * D + base + 4 * g;
+    float m, l;
+    f32x4 o[TW];
+    bool bad;  // a NaN or +inf score was seen
+
+    __device__ __forceinline__ void start(const L &ln, const float *q_row, bool col_valid) {
+        const float *qh = q_row + ln.base + 4 * ln.g;
 #pragma unroll
         for (int u = 0; u < KU; ++u) {
             const f32x4 a = *(const f32x4 *)(qh + 16 * u);
 #pragma unroll
             for (int j = 0; j < 4; ++j) qreg[u][j] = col_valid ? a[j] : 0.0f;
         }
+        m = -INFINITY;
+        l = 0.0f;
+#pragma unroll
+        for (int i = 0; i < TW; ++i) o[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
 
-    __shared__ f32x4 sx[2][2][NW][64];  // partial S^T of a pair, double-buffered
-
-    float m = -INFINITY, l = 0.0f;  // reference maximum, sum of exp relative to it
-    bool bad = false;
-    f32x4 o[TW];
-#pragma unroll
-    for (int i = 0; i < TW; ++i) o[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    int buf = 0;
-
-    auto compute_pair = [&](int q, const KvTile<D> (&P)[2]) {
+    // One pair of tiles (32 keys) with `valid` of its keys in range: the two
+    // score chains, the cross-wave sum, the softmax bookkeeping and the P.V
+    // chains of a pair run together, so each fixed latency -- the barrier,
+    // the LDS round trip, the softmax's dependent steps -- is paid once per
+    // 32 keys.
+    __device__ __forceinline__ void pair(const L &ln, const KvTile<D> (&P)[2], int valid, float scale,
+                                         PairScores<D> &sx, int &buf) {
         // Partial S^T of both tiles over this wave's dims (two MFMA chains).
         f32x4 acc[2] = {};
 #pragma unroll
@@ -334,15 +322,15 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::NW) void decode_split_kernel(D
 
         // The tiles' S^T: the waves' partials summed in a fixed order, so
         // every wave holds the same bits (all reads issue before the first add).
-        sx[buf][0][wave][lane] = acc[0];
-        sx[buf][1][wave][lane] = acc[1];
+        sx[buf][0][ln.wave][ln.lane] = acc[0];
+        sx[buf][1][ln.wave][ln.lane] = acc[1];
         __syncthreads();
         f32x4 sc[2];
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             f32x4 v[NW];
 #pragma unroll
-            for (int w = 0; w < NW; ++w) v[w] = sx[buf][t][w][lane];
+            for (int w = 0; w < NW; ++w) v[w] = sx[buf][t][w][ln.lane];
             if constexpr (NW == 8)
                 sc[t] = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
             else
@@ -351,20 +339,19 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::NW) void decode_split_kernel(D
         buf ^= 1;
 
         // Scores of keys 16t + 4g + r of the pair for head c; NaN or +inf
-        // fails the call; keys past the end (last pair only) are masked.
+        // fails the call; keys past the end (a last pair) are masked.
         float sv[8];
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                sv[4 * t + r] = sc[t][r] * p.scale;
+                sv[4 * t + r] = sc[t][r] * scale;
                 bad |= __builtin_amdgcn_classf(sv[4 * t + r], 0x203);  // signalling/quiet NaN, +inf
             }
-        const int valid = n_keys - 32 * q;
         if (valid < 32) {
 #pragma unroll
             for (int k = 0; k < 8; ++k)
-                if (16 * (k >> 2) + 4 * g + (k & 3) >= valid) sv[k] = -INFINITY;
+                if (16 * (k >> 2) + 4 * ln.g + (k & 3) >= valid) sv[k] = -INFINITY;
         }
         const float mt = rows_max(fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
                                         fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7]))));
@@ -392,47 +379,221 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::NW) void decode_split_kernel(D
 #pragma unroll
                 for (int i = 0; i < TW; ++i)
                     o[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(P[t].v[r][i], pr[4 * t + r], o[i], 0, 0, 0);
-    };
+    }
 
-    // Steady state: each step issues the loads of the pair NPAIR-1 ahead
-    // (clamped into range, so every load is unconditional and the wait
-    // counts stay exact), then computes the oldest buffered pair.
-    int q0 = 0;
-    for (; q0 + NPAIR - 1 < n_pairs; q0 += NPAIR) {
+    // The attention output of head c (l summed over the lanes c, c+16, c+32,
+    // c+48); out_row = the head's D floats.  A head whose scores were all
+    // -inf fails the call.
+    __device__ __forceinline__ void write_output(const L &ln, float *out_row, bool col_valid, unsigned *status) const {
+        const float lt = rows_sum(l);
+        if (ln.wave == 0 && __any(col_valid && m == -INFINITY) && ln.lane == 0) atomicOr(status, kStatusNonFinite);
+        if (!col_valid) return;
+        const float inv = 1.0f / lt;
+        float *op = out_row + ln.base;
+#pragma unroll
+        for (int i = 0; i < TW; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) op[TW * (4 * ln.g + r) + i] = o[i][r] * inv;
+    }
+
+    // This wave's share of a split partial (see partial_dim0); `slot` is the
+    // partial's index in units of G*D floats / G (m, l) pairs.
+    __device__ __forceinline__ void write_partial(const L &ln, float *part_o, float2 *part_ml, int64_t slot, int G,
+                                                  bool col_valid) const {
+        const float lt = rows_sum(l);
+        if (!col_valid) return;
+        f32x4 *po = (f32x4 *)(part_o + slot * G * D);
+#pragma unroll
+        for (int i = 0; i < TW; ++i) po[((ln.wave * TW + i) * 4 + ln.g) * G + ln.c] = o[i];
+        if (ln.wave == 0 && ln.g == 0) part_ml[slot * G + ln.c] = float2{m, lt};
+    }
+};
+
+// Pairs q_first .. q_first + n_pairs - 1 of the rows behind (krs, vrs),
+// which hold n_keys keys, into acc.  Pairs stream through NBUF/2 register
+// slots, one pair in flight while one is computed; loads are issued
+// unconditionally (clamped to the last pair), so the compiler's wait counts
+// stay exact and never wait on a prefetch.  A pair's second tile past the
+// end (odd tile count) reads zeros and is masked.
+template <int D, int NBUF>
+__device__ __forceinline__ void run_pairs(const DecodeLane<D> &ln, DecodeAcc<D> &acc, __amdgpu_buffer_rsrc_t krs,
+                                          __amdgpu_buffer_rsrc_t vrs, int q_first, int n_pairs, int n_keys,
+                                          float scale, PairScores<D> &sx, int &buf) {
+    constexpr int NPAIR = NBUF / 2;
+    KvTile<D> T[NPAIR][2];
+    auto load_pair = [&](int i, KvTile<D> (&P)[2]) {
+        const int q = q_first + (i < n_pairs ? i : n_pairs - 1);
+        ln.load_tile(krs, vrs, 2 * q, P[0]);
+        ln.load_tile(krs, vrs, 2 * q + 1, P[1]);
+    };
+#pragma unroll
+    for (int b = 0; b < NPAIR - 1; ++b) load_pair(b, T[b]);
+    // Steady state: each step issues the loads of the pair NPAIR-1 ahead,
+    // then computes the oldest buffered pair.
+    int i0 = 0;
+    for (; i0 + NPAIR - 1 < n_pairs; i0 += NPAIR) {
 #pragma unroll
         for (int b = 0; b < NPAIR; ++b) {
-            const int pf = q0 + b + NPAIR - 1;
-            load_pair(pf < n_pairs ? pf : n_pairs - 1, T[(b + NPAIR - 1) % NPAIR]);
-            compute_pair(q0 + b, T[b]);
+            load_pair(i0 + b + NPAIR - 1, T[(b + NPAIR - 1) % NPAIR]);
+            acc.pair(ln, T[b], n_keys - 32 * (q_first + i0 + b), scale, sx, buf);
         }
     }
     // Tail: the remaining (< NPAIR) pairs are already buffered in T[0..].
 #pragma unroll
     for (int b = 0; b < NPAIR - 1; ++b)
-        if (q0 + b < n_pairs) compute_pair(q0 + b, T[b]);
+        if (i0 + b < n_pairs) acc.pair(ln, T[b], n_keys - 32 * (q_first + i0 + b), scale, sx, buf);
+}
 
-    if (wave == 0 && __any(bad && col_valid) && lane == 0) atomicOr(p.status, kStatusNonFinite);
+// One workgroup = one (split, KV head, sequence); NW wavefronts, each owning
+// DW = D/NW of the head dims.
+template <int D, int MODE, int NBUF>
+__global__ __launch_bounds__(64 * DecodeShape<D>::NW) void decode_split_kernel(DecodeK p) {
+    const int split = blockIdx.x, kvh = blockIdx.y, s = blockIdx.z;
+    const DecodeLane<D> ln((int)p.row_stride);
 
-    // Sum of exp over the split for head c (lanes c, c+16, c+32, c+48).
-    const float lt = rows_sum(l);
-
-    if (n_splits == 1) {
-        if (m == -INFINITY && wave == 0 && lane == 0) atomicOr(p.status, kStatusNonFinite);
-        if (!col_valid) return;
-        const float inv = 1.0f / lt;
-        float *op = p.out + ((int64_t)s * p.n_heads + head) * D + base;
-#pragma unroll
-        for (int i = 0; i < TW; ++i)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) op[TW * (4 * g + r) + i] = o[i][r] * inv;
+    int64_t row0, begin, end;
+    seq_range<MODE>(p, s, row0, begin, end);
+    const int64_t len = end - begin;
+    if (MODE != kSingle && (len <= 0 || len > p.max_kv_len)) {  // kSingle: checked by the host
+        if (split == 0 && kvh == 0 && threadIdx.x == 0)
+            atomicOr(p.status, len <= 0 ? kStatusNonFinite : kStatusRangeTooLong);
         return;
     }
-    if (!col_valid) return;
+    // One sequence: the grid is exactly the split count, so no branch here
+    // waits on a kernel argument before the K/V loads are issued.
+    const int64_t n_splits = MODE == kSingle ? p.max_splits : num_splits(p, len);
+    if (MODE != kSingle && split >= n_splits) return;
+    const int64_t k_lo = begin + ((int64_t)split << p.chunk_shift);
+    const int64_t k_hi = (split + 1 == n_splits) ? end : k_lo + (1LL << p.chunk_shift);
+    const int n_keys = (int)(k_hi - k_lo);
+    const int n_pairs = (n_keys + 31) >> 5;
+
+    const int stride = (int)p.row_stride;
+    const int64_t first = (row0 + k_lo) * p.row_stride + (int64_t)kvh * D;
+    const __amdgpu_buffer_rsrc_t krs = ln.rows(p.k + first, n_keys, stride);
+    const __amdgpu_buffer_rsrc_t vrs = ln.rows(p.v + first, n_keys, stride);
+
+    const bool col_valid = ln.c < p.group;
+    const int head = kvh * p.group + (col_valid ? ln.c : 0);
+    DecodeAcc<D> acc;
+    acc.bad = false;
+    acc.start(ln, p.q + ((int64_t)s * p.n_heads + head) * D, col_valid);
+    __shared__ PairScores<D> sx;
+    int buf = 0;
+    run_pairs<D, NBUF>(ln, acc, krs, vrs, 0, n_pairs, n_keys, p.scale, sx, buf);
+
+    if (ln.wave == 0 && __any(acc.bad && col_valid) && ln.lane == 0) atomicOr(p.status, kStatusNonFinite);
+    if (n_splits == 1) {
+        acc.write_output(ln, p.out + ((int64_t)s * p.n_heads + head) * D, col_valid, p.status);
+        return;
+    }
     const int64_t slot = ((int64_t)s * p.n_kv_heads + kvh) * p.max_splits + split;
-    f32x4 *po = (f32x4 *)(p.part_o + slot * p.group * D);
+    acc.write_partial(ln, p.part_o, p.part_ml, slot, p.group, col_valid);
+}
+
+// Ragged batches, streamed: the sequences' attended rows are cut into pairs
+// of 16-key tiles (32 keys), numbered sequence after sequence, and each of a
+// persistent grid of workgroups (one per CU) takes an equal run of pairs.  A
+// workgroup streams its run across sequence boundaries -- the next pairs'
+// loads are in flight while the current one is computed, whichever
+// sequence they belong to -- so every CU streams HBM from start to end
+// whatever the lengths.  A sequence that lies wholly inside one workgroup's
+// run is finished there; the runs' first and last sequences may continue in
+// the neighbouring workgroups and leave partials (slot 0: the run's first
+// sequence, slot 1: its last) that decode_merge_kernel<kStream> combines.
+constexpr int kStreamMaxSeqs = 1024;
+
+// Pairs per sequence and their running sums in LDS (pref[s] = first pair of
+// sequence s); invalid ranges count no pairs and raise the status.
+__device__ inline int stream_plan(const DecodeK &p, int *pref, int64_t *first_row, int *seq_len, bool report) {
+    const int B = p.n_seqs;
+    for (int s = threadIdx.x; s < B; s += blockDim.x) {
+        const int64_t b = p.kv_begin[s], e = p.kv_end[s], len = e - b;
+        const bool ok = len > 0 && len <= p.max_kv_len;
+        if (!ok && report) atomicOr(p.status, len <= 0 ? kStatusNonFinite : kStatusRangeTooLong);
+        first_row[s] = p.seq_row0[s] + b;
+        seq_len[s] = ok ? (int)len : 0;
+        pref[s + 1] = ok ? (int)((len + 31) >> 5) : 0;
+    }
+    if (threadIdx.x == 0) pref[0] = 0;
+    __syncthreads();
+    if (threadIdx.x < 64) {  // inclusive scan of pref[1..B] by one wavefront
+        const int lane = threadIdx.x, per = (B + 63) / 64;
+        const int lo = 1 + lane * per, hi = min(lo + per, B + 1);
+        int run = 0;
+        for (int i = lo; i < hi; ++i) {
+            run += pref[i];
+            pref[i] = run;
+        }
+        int incl = run;
 #pragma unroll
-    for (int i = 0; i < TW; ++i) po[((wave * TW + i) * 4 + g) * p.group + c] = o[i];
-    if (wave == 0 && g == 0) p.part_ml[slot * p.group + c] = float2{m, lt};
+        for (int off = 1; off < 64; off <<= 1) {
+            const int t = __shfl_up(incl, off);
+            if (lane >= off) incl += t;
+        }
+        const int excl = incl - run;
+        for (int i = lo; i < hi; ++i) pref[i] += excl;
+    }
+    __syncthreads();
+    return pref[B];
+}
+
+template <int D, int NBUF>
+__global__ __launch_bounds__(64 * DecodeShape<D>::NW) void decode_stream_kernel(DecodeK p) {
+    const int w = blockIdx.x, W = gridDim.x, kvh = blockIdx.y;
+    const DecodeLane<D> ln((int)p.row_stride);
+    const int B = p.n_seqs, G = p.group, stride = (int)p.row_stride;
+    __shared__ int pref[kStreamMaxSeqs + 1];
+    __shared__ int64_t first_row[kStreamMaxSeqs];
+    __shared__ int seq_len[kStreamMaxSeqs];
+    const int total = __builtin_amdgcn_readfirstlane(stream_plan(p, pref, first_row, seq_len, w == 0 && kvh == 0));
+    // Values read back from LDS are the same in every lane; readfirstlane
+    // keeps the cursors and buffer resources in scalar registers.
+    auto pref_at = [&](int s) { return __builtin_amdgcn_readfirstlane(pref[s]); };
+    auto len_at = [&](int s) { return __builtin_amdgcn_readfirstlane(seq_len[s]); };
+    auto row_at = [&](int s) {
+        const uint64_t r = (uint64_t)first_row[s];
+        return (int64_t)(((uint64_t)__builtin_amdgcn_readfirstlane((unsigned)(r >> 32)) << 32) |
+                         (unsigned)__builtin_amdgcn_readfirstlane((unsigned)r));
+    };
+    const int ppw = (total + W - 1) / W;
+    if (w == 0 && kvh == 0) {
+        for (int i = threadIdx.x; i <= B; i += blockDim.x) p.plan[i] = pref[i];
+        if (threadIdx.x == 0) p.plan[B + 1] = ppw;
+    }
+    const int g0 = w * ppw, g1 = min(total, g0 + ppw);
+    if (g0 >= g1) return;
+    // Sequence holding pair g (the last s with pref[s] <= g; empty ones skipped).
+    auto seq_of = [&](int g, int s) {
+        while (pref_at(s + 1) <= g) ++s;
+        return s;
+    };
+
+    __shared__ PairScores<D> sx;
+    int buf = 0;
+    DecodeAcc<D> acc;
+    acc.bad = false;
+    const bool col_valid = ln.c < G;
+    const int head = kvh * G + (col_valid ? ln.c : 0);
+    // One segment per sequence the run touches: pairs [g, ge) of sequence cs.
+    int cs = seq_of(g0, 0);
+    for (int g = g0; g < g1;) {
+        const int ga = pref_at(cs), gb = pref_at(cs + 1), ge = min(g1, gb), n_keys = len_at(cs);
+        const int64_t first = row_at(cs) * p.row_stride + (int64_t)kvh * D;
+        const __amdgpu_buffer_rsrc_t krs = ln.rows(p.k + first, n_keys, stride);
+        const __amdgpu_buffer_rsrc_t vrs = ln.rows(p.v + first, n_keys, stride);
+        acc.start(ln, p.q + ((int64_t)cs * p.n_heads + head) * D, col_valid);
+        run_pairs<D, NBUF>(ln, acc, krs, vrs, g - ga, ge - g, n_keys, p.scale, sx, buf);
+        if (g == ga && ge == gb) {
+            acc.write_output(ln, p.out + ((int64_t)cs * p.n_heads + head) * D, col_valid, p.status);
+        } else {  // slot 0: the run's first sequence; 1: its last
+            const int64_t slot = ((int64_t)(2 * w + (g == g0 ? 0 : 1))) * p.n_kv_heads + kvh;
+            acc.write_partial(ln, p.part_o, p.part_ml, slot, G, col_valid);
+        }
+        g = ge;
+        if (g < g1) cs = seq_of(g, cs);
+    }
+    if (ln.wave == 0 && __any(acc.bad && col_valid) && ln.lane == 0) atomicOr(p.status, kStatusNonFinite);
 }
 
 // Merges the split partials of one (sequence, KV head):
@@ -447,7 +608,20 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeK p) {
     const int s = blockIdx.z, kvh = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     int n = p.max_splits;
-    if constexpr (MODE != kSingle) {
+    // Partial j of this (sequence, KV head) is at slot0 + j*jslot, except for
+    // streamed batches, whose first partial may sit in its workgroup's second
+    // slot (first_extra).
+    int64_t slot0 = ((int64_t)s * p.n_kv_heads + kvh) * p.max_splits, jslot = 1, first_extra = 0;
+    if constexpr (MODE == kStream) {
+        const int ga = p.plan[s], gb = p.plan[s + 1], ppw = p.plan[p.n_seqs + 1];
+        if (gb <= ga) return;  // an invalid range: reported by the split kernel
+        const int w1 = ga / ppw, w2 = (gb - 1) / ppw;
+        if (w1 == w2) return;  // finished by its workgroup
+        n = w2 - w1 + 1;
+        slot0 = (int64_t)2 * w1 * p.n_kv_heads + kvh;
+        jslot = 2 * p.n_kv_heads;
+        first_extra = ga > w1 * ppw ? p.n_kv_heads : 0;
+    } else if constexpr (MODE != kSingle) {
         int64_t row0, begin, end;
         seq_range<MODE>(p, s, row0, begin, end);
         const int64_t len = end - begin;
@@ -456,14 +630,11 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeK p) {
     }
     if (MODE != kSingle && n <= 1) return;  // kSingle: launched only with splits
     const int G = p.group;
-    const int64_t slot0 = ((int64_t)s * p.n_kv_heads + kvh) * p.max_splits;
 
     const int ph = tid >> 4, el = tid & 15;
     const int e = blockIdx.x * 16 + el;  // stored vector index within a split
     const int c = e % G;
-    const f32x4 *src = (const f32x4 *)(p.part_o + slot0 * G * D) + e;
-    const int64_t jstride = (int64_t)G * D / 4;
-    const float2 *mlc = p.part_ml + slot0 * G + c;
+    auto slot = [&](int j) { return slot0 + j * jslot + (j == 0 ? first_extra : 0); };
 
     float mt = -INFINITY, lt = 0.0f;
     f32x4 ot = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -471,9 +642,9 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeK p) {
         float2 t[kMergeBatch];
         f32x4 v[kMergeBatch];
 #pragma unroll
-        for (int b = 0; b < kMergeBatch; ++b) t[b] = mlc[min(j0 + 16 * b, n - 1) * G];
+        for (int b = 0; b < kMergeBatch; ++b) t[b] = p.part_ml[slot(min(j0 + 16 * b, n - 1)) * G + c];
 #pragma unroll
-        for (int b = 0; b < kMergeBatch; ++b) v[b] = src[min(j0 + 16 * b, n - 1) * jstride];
+        for (int b = 0; b < kMergeBatch; ++b) v[b] = ((const f32x4 *)(p.part_o + slot(min(j0 + 16 * b, n - 1)) * G * D))[e];
         fold_batch(mt, lt, ot, t, v, j0, 16, n);
     }
     // Phases 4w..4w+3 of wave w sit 16 lanes apart.
@@ -578,6 +749,37 @@ __global__ __launch_bounds__(256) void decode_generic_kernel(DecodeK p, int D) {
 
 namespace {
 
+// Ragged batch through decode_stream_kernel: one workgroup per CU per KV head
+// (at least one), then the merge of the sequences that span workgroups.
+int launch_stream(g4_ctx *ctx, const DecodeArgs &a, DecodeK p, hipStream_t stream) {
+    const int D = a.head_dim, G = p.group;
+    const int W = ctx->num_cus / a.n_kv_heads > 0 ? ctx->num_cus / a.n_kv_heads : 1;
+    const size_t slots = (size_t)W * 2 * a.n_kv_heads;
+    const size_t o_bytes = (slots * G * D * sizeof(float) + 255) / 256 * 256;
+    const size_t ml_bytes = (slots * G * sizeof(float2) + 255) / 256 * 256;
+    int rc = ensure_workspace(ctx, o_bytes + ml_bytes + (size_t)(a.B + 2) * sizeof(int), stream);
+    if (rc != G4_OK) return rc;
+    p.part_o = (float *)ctx->ws.ptr;
+    p.part_ml = (float2 *)((char *)ctx->ws.ptr + o_bytes);
+    p.plan = (int *)((char *)ctx->ws.ptr + o_bytes + ml_bytes);
+    p.n_seqs = a.B;
+    const dim3 grid((unsigned)W, (unsigned)a.n_kv_heads);
+    if (D == 256)
+        hipLaunchKernelGGL((decode_stream_kernel<256, kDecodeBuffers>), grid, dim3(64 * DecodeShape<256>::NW), 0,
+                           stream, p);
+    else
+        hipLaunchKernelGGL((decode_stream_kernel<512, kDecodeBuffers>), grid, dim3(64 * DecodeShape<512>::NW), 0,
+                           stream, p);
+    G4_HIP(hipGetLastError());
+    const dim3 mgrid(D * G / 64, a.n_kv_heads, a.B);
+    if (D == 256)
+        hipLaunchKernelGGL((decode_merge_kernel<kStream, 256>), mgrid, dim3(256), 0, stream, p);
+    else
+        hipLaunchKernelGGL((decode_merge_kernel<kStream, 512>), mgrid, dim3(256), 0, stream, p);
+    G4_HIP(hipGetLastError());
+    return G4_OK;
+}
+
 template <int MODE>
 int launch_mode(g4_ctx *ctx, const DecodeArgs &a, DecodeK p, hipStream_t stream) {
     const int D = a.head_dim;
@@ -593,6 +795,14 @@ int launch_mode(g4_ctx *ctx, const DecodeArgs &a, DecodeK p, hipStream_t stream)
         G4_HIP(hipGetLastError());
         return G4_OK;
     }
+    // Ragged batches stream unless a split size was set explicitly or the
+    // batch is too small to give each CU a few 32-key pairs (then the split
+    // grid's shorter prologue wins); the streamed kernel addresses a
+    // sequence's rows with 32-bit byte offsets.
+    if (MODE == kBatch && ctx->decode_chunk == 0 && a.B <= kStreamMaxSeqs &&
+        (int64_t)a.B * a.max_kv_len >= 4 * 32 * (int64_t)ctx->num_cus &&
+        (a.max_kv_len + 32) * a.row_stride * (int64_t)sizeof(float) < (1LL << 31))
+        return launch_stream(ctx, a, p, stream);
 
     // Split-K sizing.  A split is a power of two of at least one 16-key
     // MFMA tile.  One sequence: about two workgroups per CU, at least 32

@@ -182,3 +182,85 @@ def test_ragged_range_longer_than_bound_is_reported(ctx):
     with pytest.raises(g4hip.EngError) as e:
         ctx.check_status()
     assert e.value.kind == "ContextTooLong"
+
+
+def _ragged_case(seed, lens, d, n_heads=8, n_kv=1, gap=3):
+    """Packed caches of several sequences (NaN rows between them) and their queries."""
+    rng = np.random.default_rng(seed)
+    B = len(lens)
+    width = n_kv * d
+    row0 = np.zeros(B, np.int64)
+    at = 0
+    for s in range(B):
+        row0[s] = at
+        at += int(lens[s]) + gap
+    K = np.full((at, width), np.nan, np.float32)
+    V = np.full((at, width), np.nan, np.float32)
+    for s in range(B):
+        K[row0[s]:row0[s] + lens[s]] = rng.standard_normal((int(lens[s]), width), dtype=np.float32)
+        V[row0[s]:row0[s] + lens[s]] = rng.standard_normal((int(lens[s]), width), dtype=np.float32)
+    q = rng.standard_normal((B, n_heads * d), dtype=np.float32) * 0.2
+    return q, K, V, row0
+
+
+# Batches with B * max_len >= 32 * 4 * 256 take the streamed path (one
+# workgroup per CU walking the concatenated 32-key pairs); smaller ones, or
+# more than 1024 sequences, the per-sequence split grid.
+@pytest.mark.parametrize("name,lens,d,n_heads,n_kv", [
+    ("stream_short_and_long", [5, 40, 20000], 256, 8, 1),
+    ("stream_one_key_each", [1, 1, 1, 1, 9000], 512, 8, 1),
+    ("stream_fewer_pairs_than_cus", [328] + [1] * 99, 256, 8, 1),
+    ("stream_many_short", list(range(1, 301)), 256, 8, 1),  # many whole sequences per workgroup
+    ("stream_two_kv_heads", [700, 33, 8000, 64, 1], 256, 16, 2),
+    ("stream_odd_pairs", [16, 48, 80, 40000, 17, 31, 33], 512, 8, 1),
+    ("split_two_short", [5, 40], 256, 8, 1),
+    ("split_one_key_each", [1, 1, 1, 1], 512, 8, 1),
+    ("split_over_stream_limit", [7] * 1030 + [300], 256, 8, 1),
+])
+def test_ragged_batch_shapes(ctx, name, lens, d, n_heads, n_kv):
+    print(f"[case] ragged {name} d={d} B={len(lens)}", flush=True)
+    lens = np.array(lens, np.int64)
+    q, K, V, row0 = _ragged_case(len(lens) * 7 + d, lens, d, n_heads, n_kv)
+    B = len(lens)
+    begin = np.zeros(B, np.int64)
+    out = torch.zeros(B * n_heads * d, device="cuda")
+    ctx.attend_decode_batch(dev(q), dev(K), dev(V), dev(row0), dev(begin), dev(lens), int(lens.max()),
+                            n_heads, n_kv, d, out)
+    ctx.check_status()
+    got = out.cpu().numpy().reshape(B, -1)
+    worst = 0.0
+    for s in range(B):
+        rows = slice(row0[s], row0[s] + lens[s])
+        worst = max(worst, I.rel_err(got[s], orc.attend(q[s], K[rows], V[rows], n_heads, n_kv)))
+    print(f"[parity] ragged {name}: worst rel err {worst:.2e}")
+    assert worst <= TOL
+
+
+def test_ragged_batch_with_set_split_size(ctx):
+    """A split size set by the caller selects the per-sequence split grid."""
+    lens = np.array([1500, 20, 333, 4096, 1], np.int64)
+    d = 512
+    q, K, V, row0 = _ragged_case(77, lens, d)
+    out = torch.zeros(len(lens) * 8 * d, device="cuda")
+    ctx.set_decode_chunk(64)
+    try:
+        ctx.attend_decode_batch(dev(q), dev(K), dev(V), dev(row0), dev(np.zeros(len(lens), np.int64)), dev(lens),
+                                int(lens.max()), 8, 1, d, out)
+        ctx.check_status()
+    finally:
+        ctx.set_decode_chunk(0)
+    got = out.cpu().numpy().reshape(len(lens), -1)
+    for s in range(len(lens)):
+        rows = slice(row0[s], row0[s] + lens[s])
+        assert I.rel_err(got[s], orc.attend(q[s], K[rows], V[rows], 8, 1)) <= TOL
+
+
+def test_ragged_empty_range_is_an_error(ctx):
+    lens = np.array([100, 0, 50], np.int64)
+    d = 256
+    q, K, V, row0 = _ragged_case(5, np.maximum(lens, 1), d)
+    out = torch.zeros(3 * 8 * d, device="cuda")
+    ctx.attend_decode_batch(dev(q), dev(K), dev(V), dev(row0), dev(np.zeros(3, np.int64)), dev(lens), 100, 8, 1, d,
+                            out)
+    with pytest.raises(g4hip.EngError, match="softmax input is not finite"):
+        ctx.check_status()
