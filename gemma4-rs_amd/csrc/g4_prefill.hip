@@ -33,6 +33,9 @@ namespace {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
+// s_waitcnt operand: vector memory count 0 (the LDS-bound tile loads have
+// landed), export and LDS/scalar counts left at their maxima.
+constexpr int kVmcntZero = 0x0F70;
 constexpr int kRowsPerWave = 16;
 constexpr int kWaves = 4;
 constexpr int kPosPerWave = 2;                       // 16 rows = 2 positions x 8 heads
@@ -40,6 +43,9 @@ constexpr int kPosPerBlock = kWaves * kPosPerWave;   // 8
 constexpr int kGroup = 8;                            // query heads per KV head
 constexpr float kRescaleSlack = 8.0f / 1.4426950408889634f;  // 8 in log2 units
 constexpr int kPrefillMaxUnitsDev = 8;  // partial units per block (merge weight table)
+// Buffer resource (V#) word 3 for raw 32-bit-element buffers on gfx9-class
+// GPUs, gfx950 included.
+constexpr int kBufferWord3 = 0x00020000;
 
 struct PrefillUnit {
     int block;   // position block: positions pos0 + 8*block .. +7
@@ -71,6 +77,45 @@ struct PrefillK {
 };
 
 __device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Reductions over the four 16-lane rows of a wavefront (lanes c, c+16,
+// c+32, c+48), done with row swaps on the VALU and identical in every lane.
+__device__ inline float rows_max(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    const float h = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(h), __float_as_uint(h), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ inline float rows_sum(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    const float h = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(h), __float_as_uint(h), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// s_waitcnt operand: LDS/scalar count 0 (this wave's ds_writes are done),
+// vector memory and export counts left at their maxima.
+constexpr int kLgkmcntZero = 0xC07F;
+
+// Workgroup barrier after this wave's own LDS writes: they are complete
+// (lgkm count 0) before the barrier, and the signal fences keep the compiler
+// from moving LDS accesses across it.  Unlike __syncthreads(), whose fence
+// also waits for the next tile's LDS-bound loads (they write LDS), those
+// stay in flight; nothing read after this barrier is written by them.
+__device__ inline void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(kLgkmcntZero);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// One 16-byte load per lane from `rsrc` at byte offset voff, written straight
+// to LDS at lds + 16 * lane (lds is the same for the whole wavefront).
+__device__ inline void load_to_lds(__amdgpu_buffer_rsrc_t rsrc, f32x4 *lds, uint32_t voff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void *)lds, 16, voff, 0, 0, 0);
+#endif
+}
 
 // Workgroup geometry for head width D: 4 row groups of 16 rows, each owned by
 // SPLIT wavefronts that divide the head dimension (DH = D / SPLIT dims each),
@@ -108,51 +153,51 @@ __global__ __launch_bounds__(PrefillShape<D>::THREADS, 1) void prefill_kernel(Pr
     const int64_t win = p.window;
     const int d0 = half * DH;  // first dim of this wave
 
-    // One array for both tiles, [buf][0] = K in the swizzle of stage_k,
-    // [buf][1] = V row-major [key][D/4]; the epilogue reuses all of it
-    // (2*2*TILE_F4 float4 = 64*D floats) to transpose the output rows.
-    __shared__ f32x4 lds_kv[2][2][TILE_F4];
-    __shared__ f32x4 lds_s[2][S::WAVES][64];  // partial S^T of the D halves
+    // Double-buffered K and V tiles and partial S^T of the D halves, each
+    // buffer its own array: the tile being loaded and the tile being read
+    // are then distinct objects, so the compiler need not wait for the
+    // former's loads before reading the latter.  The epilogue reuses the
+    // four tile arrays (64*D floats) to transpose the output rows.
+    __shared__ f32x4 lds_k0[TILE_F4], lds_v0[TILE_F4], lds_k1[TILE_F4], lds_v1[TILE_F4];
+    __shared__ f32x4 lds_s0[S::WAVES][64], lds_s1[S::WAVES][64];
 
-    // K/V tile loaders: thread tid loads float4 f = tid + THREADS*e of the
-    // tile (row f / (D/4), dims 4*(f % (D/4)) ..).  Rows past the last
-    // position are clamped (masked for every query of the chunk); rows before
-    // the block's first window start are outside every row's attended set and
-    // are staged as zeros, so whatever they hold cannot reach the output
-    // through a zero softmax weight (0 * NaN).  K and V of the next tile are
-    // fetched at different points of the current one, so that only half a
-    // tile is held in registers at a time.
-    const float *kbase = p.k + (int64_t)kvh * D;
-    const float *vbase = p.v + (int64_t)kvh * D;
+    // K/V tiles go straight from memory to LDS (buffer_load ... lds: lane l
+    // of a wavefront writes the 16 bytes it loads to LDS base + 16*l), so the
+    // LDS layout is chosen by which address each lane loads: thread tid fills
+    // float4 slot f = (e*WAVES + wave)*64 + lane of the tile, e < PER_THREAD.
+    // K slots are swizzled -- ((u*4 + g)*2 + h)*16 + key holds dims
+    // 32u + 8g + 4h .. +3 -- so the 16 lanes reading a quarter MFMA operand
+    // read 256 contiguous bytes; V slots are row-major [key][D/4].  The
+    // resources span the rows some query of this block attends, [block_lo,
+    // last_pos]; every other row of a tile (before the window, past the
+    // chunk) reads as zeros in hardware, so nothing it holds can reach the
+    // output through a zero softmax weight (0 * NaN).  The tile's offset goes
+    // into the per-lane offset, which the range check covers.
+    const int stride = (int)p.row_stride;  // (pos0 + N) rows of it span < 2^31 bytes (checked by the launcher)
     const int64_t block_lo = (win > 0 && P0 + 1 > win) ? P0 + 1 - win : 0;
-    f32x4 rx[PER_THREAD];
-    auto fetch = [&](const float *base, int t) {
+    const int n_rows = (int)(last_pos + 1 - block_lo);
+    const float *first_row = p.k + block_lo * p.row_stride + (int64_t)kvh * D;
+    const __amdgpu_buffer_rsrc_t krs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)first_row, 0, (n_rows - 1) * stride * 4 + D * 4, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(p.v + block_lo * p.row_stride + (int64_t)kvh * D), 0, (n_rows - 1) * stride * 4 + D * 4, kBufferWord3);
+    uint32_t koffs[PER_THREAD], voffs[PER_THREAD];
+#pragma unroll
+    for (int e = 0; e < PER_THREAD; ++e) {
+        const int f = (e * S::WAVES + wave) * 64 + lane;
+        const int key = f & 15, rest = f >> 4;
+        const int dim = 32 * (rest >> 3) + 8 * ((rest >> 1) & 3) + 4 * (rest & 1);
+        koffs[e] = (uint32_t)(key * stride + dim) * 4u;
+        voffs[e] = (uint32_t)((f / (D / 4)) * stride + 4 * (f % (D / 4))) * 4u;
+    }
+    auto issue_tile = [&](int t, f32x4 *kb, f32x4 *vb) {
+        const uint32_t toff = (uint32_t)((16LL * t - block_lo) * stride * 4);  // wraps below block_lo: out of range
 #pragma unroll
         for (int e = 0; e < PER_THREAD; ++e) {
-            const int f = tid + S::THREADS * e;
-            const int row = f / (D / 4), c4 = f % (D / 4);
-            int64_t key = 16LL * t + row;
-            const bool stale = key < block_lo;
-            if (key > last_pos) key = last_pos;
-            const f32x4 x = *(const f32x4 *)(base + key * p.row_stride + 4 * c4);
-            rx[e] = stale ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : x;
+            const int slot = (e * S::WAVES + wave) * 64;
+            load_to_lds(krs, kb + slot, koffs[e] + toff);
+            load_to_lds(vrs, vb + slot, voffs[e] + toff);
         }
-    };
-    auto stage_k = [&](int buf) {
-#pragma unroll
-        for (int e = 0; e < PER_THREAD; ++e) {
-            const int f = tid + S::THREADS * e;
-            const int row = f / (D / 4), c4 = f % (D / 4);
-            const int dim = 4 * c4;
-            const int uu = dim >> 5, gg = (dim >> 3) & 3, hh = (dim >> 2) & 1;
-            // The 16 lanes reading one quarter of an MFMA operand read 256
-            // contiguous bytes: index ((u*4 + g)*2 + h)*16 + key.
-            lds_kv[buf][0][((uu * 4 + gg) * 2 + hh) * 16 + row] = rx[e];
-        }
-    };
-    auto stage_v = [&](int buf) {
-#pragma unroll
-        for (int e = 0; e < PER_THREAD; ++e) lds_kv[buf][1][tid + S::THREADS * e] = rx[e];
     };
 
     // Q^T (B operand): lane (g, c) holds q[row c][d0 + 32u + 8g + j].
@@ -178,25 +223,21 @@ __global__ __launch_bounds__(PrefillShape<D>::THREADS, 1) void prefill_kernel(Pr
     float m = -INFINITY, l = 0.0f;
     bool bad = false;
 
-    fetch(kbase, u.t_lo);
-    stage_k(0);
-    fetch(vbase, u.t_lo);
-    stage_v(0);
-    int buf = 0;
-    for (int t = u.t_lo; t < u.t_hi; ++t) {
-        // The next tile (the current one again on the last step, so that the
-        // loads are unconditional and the compiler's wait counts stay exact).
-        const int tn = t + 1 < u.t_hi ? t + 1 : t;
-        fetch(kbase, tn);  // in flight during this tile's QK^T
-        __syncthreads();   // tile t staged in lds[buf]; buf^1 free
+    // Tile t is read from (kb, vb) while tile t+1 loads into (kn, vn).
+    auto step = [&](int t, const f32x4 *kb, const f32x4 *vb, f32x4 (*ls)[64], f32x4 *kn, f32x4 *vn) {
+        // Tile t has landed (this wave's loads, then everyone's), and every
+        // wave is done reading (kn, vn): fetch tile t+1 into them.
+        __builtin_amdgcn_s_waitcnt(kVmcntZero);
+        __syncthreads();
+        if (t + 1 < u.t_hi) issue_tile(t + 1, kn, vn);
 
         // Partial S^T over this wave's DH dims: two independent chains.
         f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int uu = 0; uu < NU; ++uu) {
             const int ug = d0 / 32 + uu;
-            const f32x4 k0 = lds_kv[buf][0][((ug * 4 + g) * 2 + 0) * 16 + c];
-            const f32x4 k1 = lds_kv[buf][0][((ug * 4 + g) * 2 + 1) * 16 + c];
+            const f32x4 k0 = kb[((ug * 4 + g) * 2 + 0) * 16 + c];
+            const f32x4 k1 = kb[((ug * 4 + g) * 2 + 1) * 16 + c];
             f32x4 &acc = (uu & 1) ? acc1 : acc0;
 #pragma unroll
             for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k0[j], qreg[uu][j], acc, 0, 0, 0);
@@ -206,27 +247,28 @@ __global__ __launch_bounds__(PrefillShape<D>::THREADS, 1) void prefill_kernel(Pr
         f32x4 sc = acc0 + acc1;
         if constexpr (S::SPLIT == 2) {
             // Full scores = half 0 + half 1, added in that order by both waves.
-            lds_s[buf][wave][lane] = sc;
-            __syncthreads();
-            sc = lds_s[buf][rg][lane] + lds_s[buf][rg + kWaves][lane];
+            ls[wave][lane] = sc;
+            lds_barrier();
+            sc = ls[rg][lane] + ls[rg + kWaves][lane];
         }
-        stage_k(buf ^ 1);
-        fetch(vbase, tn);  // in flight during softmax and P.V
 
-        // Exact attended set per row: key <= pos and, with a window, key > pos - W.
+        // Exact attended set per row: key <= pos and, with a window, key >
+        // pos - W.  Tiles every row of the block sees whole skip the test.
         float sv[4];
-        float mt = -INFINITY;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int64_t key = 16LL * t + 4 * g + r;
-            const bool vis = key <= pos && (win == 0 || key > pos - win);
-            const float x = sc[r] * p.scale;
-            bad |= vis && ((x != x) || (x == INFINITY));
-            sv[r] = vis ? x : -INFINITY;
-            mt = fmaxf(mt, sv[r]);
+        for (int r = 0; r < 4; ++r) sv[r] = sc[r] * p.scale;
+        const bool whole = 16LL * t + 15 <= P0 && (win == 0 || 16LL * t > P0 + kPosPerBlock - 1 - win);
+        if (!whole) {
+            const int64_t rel = pos - 16LL * t;  // key - 16t <= rel, and > rel - win
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int kr = 4 * g + r;
+                if (!(kr <= rel && (win == 0 || kr > rel - win))) sv[r] = -INFINITY;
+            }
         }
-        mt = fmaxf(mt, __shfl_xor(mt, 16));
-        mt = fmaxf(mt, __shfl_xor(mt, 32));
+#pragma unroll
+        for (int r = 0; r < 4; ++r) bad |= __builtin_amdgcn_classf(sv[r], 0x203);  // signalling/quiet NaN, +inf
+        const float mt = rows_max(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])));
         // Lazy rescaling: a row keeps its reference max m until a score
         // exceeds it by more than kRescaleSlack (p <= 2^8 meanwhile, safe in
         // f32), so O is rescaled a few times per row rather than every tile.
@@ -248,19 +290,22 @@ __global__ __launch_bounds__(PrefillShape<D>::THREADS, 1) void prefill_kernel(Pr
         for (int r = 0; r < 4; ++r)
 #pragma unroll
             for (int U = 0; U < NV; ++U) {
-                const f32x4 vv = lds_kv[buf][1][(4 * g + r) * (D / 4) + d0 / 4 + 16 * U + c];
+                const f32x4 vv = vb[(4 * g + r) * (D / 4) + d0 / 4 + 16 * U + c];
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
                     o[4 * U + i] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[i], pr[r], o[4 * U + i], 0, 0, 0);
             }
-
-        stage_v(buf ^ 1);  // buf^1 was last read before this tile's first barrier
-        buf ^= 1;
+    };
+    issue_tile(u.t_lo, lds_k0, lds_v0);
+    int t = u.t_lo;
+    for (; t + 1 < u.t_hi; t += 2) {
+        step(t, lds_k0, lds_v0, lds_s0, lds_k1, lds_v1);
+        step(t + 1, lds_k1, lds_v1, lds_s1, lds_k0, lds_v0);
     }
+    if (t < u.t_hi) step(t, lds_k0, lds_v0, lds_s0, lds_k1, lds_v1);
 
     if (__any(bad && row_valid) && lane == 0) atomicOr(p.status, kStatusNonFinite);
-    float lt = l + __shfl_xor(l, 16);
-    lt = lt + __shfl_xor(lt, 32);
+    const float lt = rows_sum(l);
 
     if (u.slot >= 0) {  // partial of a multi-unit block, in the accumulator layout
         const int64_t sl = (int64_t)u.slot * gridDim.y + kvh;
@@ -271,9 +316,12 @@ __global__ __launch_bounds__(PrefillShape<D>::THREADS, 1) void prefill_kernel(Pr
         return;
     }
     // Single unit: normalise and write row-major through LDS (coalesced).
-    __syncthreads();  // every wave is done with the tile buffers
-    static_assert(S::WAVES * kRowsPerWave * DH <= 2 * 2 * TILE_F4 * 4, "transpose fits the tile buffers");
-    float *tr = (float *)&lds_kv[0][0][0] + wave * (kRowsPerWave * DH);
+    __syncthreads();  // every wave is done with the tile buffers (no tile load is in flight)
+    // Two waves' rows per tile array.
+    static_assert(2 * kRowsPerWave * DH <= TILE_F4 * 4 && S::WAVES == 8, "transpose fits the tile buffers");
+    const int ta = wave >> 1;
+    f32x4 *tb = ta == 0 ? lds_k0 : ta == 1 ? lds_v0 : ta == 2 ? lds_k1 : lds_v1;
+    float *tr = (float *)tb + (wave & 1) * (kRowsPerWave * DH);
     const float inv = 1.0f / lt;
 #pragma unroll
     for (int U = 0; U < NV; ++U)
@@ -447,8 +495,10 @@ static int build_plan(g4_ctx *ctx, const PrefillArgs &a, PrefillPlan &pl) {
 
 int launch_prefill(g4_ctx *ctx, const PrefillArgs &a, hipStream_t stream) {
     const int group = a.n_heads / a.n_kv_heads;
+    // The MFMA kernel addresses a block's rows with 32-bit byte offsets.
     const bool mfma = (a.head_dim == 256 || a.head_dim == 512) && group == kGroup &&
-                      a.n_heads % a.n_kv_heads == 0;
+                      a.n_heads % a.n_kv_heads == 0 &&
+                      (a.pos0 + a.N + 16) * a.row_stride * (int64_t)sizeof(float) < (1LL << 31);
     if (!mfma) {
         // Any other shape: every query as an independent decode over its range.
         DecodeArgs d{};
