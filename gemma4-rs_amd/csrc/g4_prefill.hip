@@ -122,7 +122,7 @@ __device__ inline void load_to_lds(__amdgpu_buffer_rsrc_t rsrc, f32x4 *lds, uint
 // so that one wavefront's Q^T and O^T fit the register file.
 template <int D>
 struct PrefillShape {
-    static constexpr int SPLIT = 2;  // merge grid's z extent is kWaves * SPLIT
+    static constexpr int SPLIT = 2;  // the merge grid's z extent is WAVES
     static constexpr int DH = D / SPLIT;
     static constexpr int WAVES = kWaves * SPLIT;
     static constexpr int THREADS = 64 * WAVES;
@@ -190,14 +190,18 @@ __global__ __launch_bounds__(PrefillShape<D>::THREADS, 1) void prefill_kernel(Pr
         koffs[e] = (uint32_t)(key * stride + dim) * 4u;
         voffs[e] = (uint32_t)((f / (D / 4)) * stride + 4 * (f % (D / 4))) * 4u;
     }
-    auto issue_tile = [&](int t, f32x4 *kb, f32x4 *vb) {
+    // Load i (of 2*PER_THREAD) of tile t: K slots for even i, V for odd.
+    auto issue_part = [&](int t, int i, f32x4 *kb, f32x4 *vb) {
         const uint32_t toff = (uint32_t)((16LL * t - block_lo) * stride * 4);  // wraps below block_lo: out of range
-#pragma unroll
-        for (int e = 0; e < PER_THREAD; ++e) {
-            const int slot = (e * S::WAVES + wave) * 64;
-            load_to_lds(krs, kb + slot, koffs[e] + toff);
+        const int e = i >> 1, slot = (e * S::WAVES + wave) * 64;
+        if (i & 1)
             load_to_lds(vrs, vb + slot, voffs[e] + toff);
-        }
+        else
+            load_to_lds(krs, kb + slot, koffs[e] + toff);
+    };
+    auto issue_tile = [&](int t, f32x4 *kb, f32x4 *vb) {
+#pragma unroll
+        for (int i = 0; i < 2 * PER_THREAD; ++i) issue_part(t, i, kb, vb);
     };
 
     // Q^T (B operand): lane (g, c) holds q[row c][d0 + 32u + 8g + j].
@@ -229,12 +233,25 @@ __global__ __launch_bounds__(PrefillShape<D>::THREADS, 1) void prefill_kernel(Pr
         // wave is done reading (kn, vn): fetch tile t+1 into them.
         __builtin_amdgcn_s_waitcnt(kVmcntZero);
         __syncthreads();
-        if (t + 1 < u.t_hi) issue_tile(t + 1, kn, vn);
+        // The last step loads its own tile again (unread), keeping every
+        // step's loads unconditional.
+        const int tn = t + 1 < u.t_hi ? t + 1 : t;
 
         // Partial S^T over this wave's DH dims: two independent chains.
         f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int uu = 0; uu < NU; ++uu) {
+            // The next tile's loads go out one or two per 8 MFMAs, so that
+            // they issue while the matrix pipe works rather than queue up
+            // behind each other at the top of the step.
+            static_assert(2 * PER_THREAD % NU == 0 || NU % (2 * PER_THREAD) == 0, "loads spread over the chunks");
+            if constexpr (2 * PER_THREAD >= NU) {
+#pragma unroll
+                for (int i = uu * (2 * PER_THREAD / NU); i < (uu + 1) * (2 * PER_THREAD / NU); ++i)
+                    issue_part(tn, i, kn, vn);
+            } else if (uu % (NU / (2 * PER_THREAD)) == 0) {
+                issue_part(tn, uu / (NU / (2 * PER_THREAD)), kn, vn);
+            }
             const int ug = d0 / 32 + uu;
             const f32x4 k0 = kb[((ug * 4 + g) * 2 + 0) * 16 + c];
             const f32x4 k1 = kb[((ug * 4 + g) * 2 + 1) * 16 + c];
@@ -243,6 +260,12 @@ __global__ __launch_bounds__(PrefillShape<D>::THREADS, 1) void prefill_kernel(Pr
             for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k0[j], qreg[uu][j], acc, 0, 0, 0);
 #pragma unroll
             for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k1[j], qreg[uu][4 + j], acc, 0, 0, 0);
+        }
+        // Scheduling: one load per 8 MFMAs of the chunk loop above.
+#pragma unroll
+        for (int uu = 0; uu < NU; ++uu) {
+            __builtin_amdgcn_sched_group_barrier(0x010, 2 * PER_THREAD >= NU ? 2 * PER_THREAD / NU : 1, 0);  // VMEM
+            __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);                                                // MFMA
         }
         f32x4 sc = acc0 + acc1;
         if constexpr (S::SPLIT == 2) {
@@ -307,6 +330,7 @@ __global__ __launch_bounds__(PrefillShape<D>::THREADS, 1) void prefill_kernel(Pr
     if (__any(bad && row_valid) && lane == 0) atomicOr(p.status, kStatusNonFinite);
     const float lt = rows_sum(l);
 
+    __builtin_amdgcn_s_waitcnt(kVmcntZero);  // the last step's spare loads have landed
     if (u.slot >= 0) {  // partial of a multi-unit block, in the accumulator layout
         const int64_t sl = (int64_t)u.slot * gridDim.y + kvh;
         f32x4 *po = (f32x4 *)(p.part_o + sl * (kWaves * kRowsPerWave * D));
@@ -317,11 +341,12 @@ __global__ __launch_bounds__(PrefillShape<D>::THREADS, 1) void prefill_kernel(Pr
     }
     // Single unit: normalise and write row-major through LDS (coalesced).
     __syncthreads();  // every wave is done with the tile buffers (no tile load is in flight)
-    // Two waves' rows per tile array.
-    static_assert(2 * kRowsPerWave * DH <= TILE_F4 * 4 && S::WAVES == 8, "transpose fits the tile buffers");
-    const int ta = wave >> 1;
+    // WAVES/4 waves' rows per tile array.
+    constexpr int WPA = S::WAVES / 4;
+    static_assert(WPA * kRowsPerWave * DH <= TILE_F4 * 4 && S::WAVES % 4 == 0, "transpose fits the tile buffers");
+    const int ta = wave / WPA;
     f32x4 *tb = ta == 0 ? lds_k0 : ta == 1 ? lds_v0 : ta == 2 ? lds_k1 : lds_v1;
-    float *tr = (float *)tb + (wave & 1) * (kRowsPerWave * DH);
+    float *tr = (float *)tb + (wave % WPA) * (kRowsPerWave * DH);
     const float inv = 1.0f / lt;
 #pragma unroll
     for (int U = 0; U < NV; ++U)
@@ -553,11 +578,15 @@ int launch_prefill(g4_ctx *ctx, const PrefillArgs &a, hipStream_t stream) {
         hipLaunchKernelGGL(prefill_kernel<512>, grid, dim3(PrefillShape<512>::THREADS), 0, stream, p);
     G4_HIP(hipGetLastError());
     if (pl.n_slots > 0) {
-        dim3 mgrid((unsigned)pl.n_blocks, (unsigned)a.n_kv_heads, (unsigned)(kWaves * 2));
+        // One merge workgroup per producing wavefront of a block.
         if (D == 256)
-            hipLaunchKernelGGL(prefill_merge_kernel<256>, mgrid, dim3(256), 0, stream, p);
+            hipLaunchKernelGGL(prefill_merge_kernel<256>,
+                               dim3((unsigned)pl.n_blocks, (unsigned)a.n_kv_heads, (unsigned)PrefillShape<256>::WAVES),
+                               dim3(256), 0, stream, p);
         else
-            hipLaunchKernelGGL(prefill_merge_kernel<512>, mgrid, dim3(256), 0, stream, p);
+            hipLaunchKernelGGL(prefill_merge_kernel<512>,
+                               dim3((unsigned)pl.n_blocks, (unsigned)a.n_kv_heads, (unsigned)PrefillShape<512>::WAVES),
+                               dim3(256), 0, stream, p);
         G4_HIP(hipGetLastError());
     }
     return G4_OK;
