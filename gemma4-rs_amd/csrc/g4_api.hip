@@ -485,6 +485,100 @@ void g4_proportional_rope_freq_factors(int head_dim, float p, float *out) {
     for (int pair = 0; pair < head_dim / 2; ++pair) out[pair] = pair < rotated ? 1.0f : 1e30f;
 }
 
+// -------------------------------------------------- fused input preparation
+namespace {
+
+int context_too_long(int64_t got, int64_t max) {
+    return g4::set_error(G4_ERR_CONTEXT_TOO_LONG,
+                         "context length " + std::to_string(got) + " exceeds configured max " + std::to_string(max),
+                         (uint64_t)got, (uint64_t)max);
+}
+
+// Validates and launches the fused preparation (model.rs:394-406).
+int prepare(g4_ctx *ctx, float *q, float *k, float *v, int64_t n_tokens, int64_t pos0, int n_heads,
+            int n_kv_heads, int head_dim, const float *q_w, const float *k_w, float eps, float base,
+            const float *factors, float *k_rows, float *v_rows, int64_t row_stride, hipStream_t stream) {
+    if (!ctx || !q) return invalid("g4_prepare_qkv: null argument");
+    if (n_tokens < 0 || pos0 < 0) return invalid("g4_prepare_qkv: negative token count or position");
+    if (n_heads <= 0 || head_dim <= 0 || (k && (n_kv_heads <= 0 || !v)))
+        return invalid("g4_prepare_qkv: needs positive head counts and head width");
+    if ((k_rows || v_rows) && (!k || !k_rows || !v_rows || row_stride < (int64_t)n_kv_heads * head_dim))
+        return invalid("g4_prepare_qkv: cache rows need k, v and a row_stride of at least the row width");
+    // ops.rs:46-48
+    if (eps < 0.0f) return g4::set_error(G4_ERR_COMPUTE, "invalid RMS norm inputs");
+    // ops.rs:142-149 with n_rot = head_dim (rope_heads, model.rs:301)
+    if (head_dim % 2 != 0 || base <= 0.0f) return g4::set_error(G4_ERR_COMPUTE, "invalid RoPE inputs");
+    g4::PrepareArgs a{};
+    a.q = q;
+    a.k = k;
+    a.v = k ? v : nullptr;
+    a.k_rows = k_rows;
+    a.v_rows = v_rows;
+    a.row_stride = row_stride;
+    a.q_w = q_w;
+    a.k_w = k_w;
+    a.factors = factors;
+    a.n_tokens = n_tokens;
+    a.pos0 = pos0;
+    a.n_heads = n_heads;
+    a.n_kv_heads = n_kv_heads;
+    a.head_dim = head_dim;
+    a.eps = eps;
+    // rope_neox computes base.powf(-2.0 / n_rot) on the host's libm (ops.rs:151).
+    a.theta_scale = powf(base, -2.0f / (float)head_dim);
+    return g4::launch_prepare_qkv(a, stream);
+}
+
+// The layer's attention set-up shared by the decode and prefill drivers:
+// kind, head width, RoPE base/divisors and the K/V source layer.
+struct LayerPlan {
+    bool global;
+    int head_dim;
+    float base;
+    const float *factors;
+    int source;
+};
+
+int plan_layer(const g4_hparams *hp, int layer, const float *rope_freqs, LayerPlan &pl) {
+    pl.global = g4_layer_is_global(hp->n_layers, layer) != 0;
+    pl.head_dim = pl.global ? hp->head_dim_global : hp->head_dim_local;
+    pl.base = pl.global ? hp->global_rope_base : hp->local_rope_base;
+    pl.factors = pl.global ? rope_freqs : nullptr;
+    // model.rs:398
+    return g4_kv_source_layer(hp->n_layers, hp->shared_kv_layers, layer, &pl.source);
+}
+
+// Reserves rows [rows, rows + n) of an owner layer's cache for a fused
+// append; the row count moves only after the launch succeeded.
+int owner_rows(g4_kv_cache *c, int layer, int64_t row_width, int64_t n, float **k_rows, float **v_rows) {
+    if (layer >= c->n_layers || c->width[layer] <= 0) return invalid("g4_kv_append: layer keeps no K/V");
+    if (c->width[layer] != row_width)
+        return invalid("g4_layer_attention: the layer's cache width differs from n_kv_heads*head_dim");
+    if (c->rows[layer] + n > c->capacity) return context_too_long(c->rows[layer] + n, c->capacity);
+    *k_rows = c->k[layer] + c->rows[layer] * row_width;
+    *v_rows = c->v[layer] + c->rows[layer] * row_width;
+    return G4_OK;
+}
+
+void commit_rows(g4_kv_cache *c, int layer, int64_t n) {
+    c->rows[layer] += n;
+    // context_memory.rs:44-47: appending to layer L makes layers 0..=L exist.
+    if (layer + 1 > c->known_layers) c->known_layers = layer + 1;
+}
+
+}  // namespace
+
+int g4_prepare_qkv(g4_ctx *ctx, float *q, float *k, float *v, int64_t n_tokens, int64_t pos0, int n_heads,
+                   int n_kv_heads, int head_dim, const float *q_norm_w, const float *k_norm_w, float eps,
+                   float rope_base, const float *freq_factors, float *k_rows, float *v_rows, int64_t row_stride,
+                   g4_stream stream) {
+    return guarded([&] {
+        g4::clear_error();
+        return prepare(ctx, q, k, v, n_tokens, pos0, n_heads, n_kv_heads, head_dim, q_norm_w, k_norm_w, eps,
+                       rope_base, freq_factors, k_rows, v_rows, row_stride, as_stream(stream));
+    });
+}
+
 // --------------------------------------------------------- layer attention
 int g4_layer_attention(g4_ctx *ctx, g4_kv_cache *cache, const g4_hparams *hp, int layer,
                        int64_t position, float *q, float *k, float *v, const float *q_norm_w,
@@ -495,48 +589,86 @@ int g4_layer_attention(g4_ctx *ctx, g4_kv_cache *cache, const g4_hparams *hp, in
         if (!ctx || !cache || !hp) return invalid("g4_layer_attention: null argument");
         if (layer < 0 || layer >= hp->n_layers) return invalid("g4_layer_attention: layer outside n_layers");
         if (position < 0) return invalid("g4_layer_attention: negative position");
-        const bool global = g4_layer_is_global(hp->n_layers, layer) != 0;
-        const int head_dim = global ? hp->head_dim_global : hp->head_dim_local;
-        const float base = global ? hp->global_rope_base : hp->local_rope_base;
-        const float *factors = global ? rope_freqs : nullptr;
-        const int64_t n_factors = factors ? head_dim / 2 : 0;
-        const hipStream_t st = as_stream(stream);
-        // model.rs:395-396
-        int rc = g4_rms_norm_rows(ctx, q, hp->n_heads, head_dim, q_norm_w, hp->rms_norm_eps, q, stream);
-        if (rc == G4_OK)
-            rc = g4_rope_neox_rows(ctx, q, 1, hp->n_heads, head_dim, head_dim, position, base, factors,
-                                   n_factors, stream);
+        LayerPlan pl;
+        int rc = plan_layer(hp, layer, rope_freqs, pl);
         if (rc != G4_OK) return rc;
-        // model.rs:398
-        int source = 0;
-        rc = g4_kv_source_layer(hp->n_layers, hp->shared_kv_layers, layer, &source);
-        if (rc != G4_OK) return rc;
-        if (source == layer) {  // model.rs:399-406
-            rc = g4_rms_norm_rows(ctx, k, hp->n_kv_heads, head_dim, k_norm_w, hp->rms_norm_eps, k, stream);
-            if (rc == G4_OK)
-                rc = g4_rms_norm_rows(ctx, v, hp->n_kv_heads, head_dim, nullptr, hp->rms_norm_eps, v, stream);
-            if (rc == G4_OK)
-                rc = g4_rope_neox_rows(ctx, k, 1, hp->n_kv_heads, head_dim, head_dim, position, base,
-                                       factors, n_factors, stream);
-            if (rc == G4_OK) rc = g4_kv_append(cache, layer, k, v, stream);
+        const int head_dim = pl.head_dim;
+        const int64_t row_width = (int64_t)hp->n_kv_heads * head_dim;
+        const bool owner = pl.source == layer;
+        // model.rs:394-406 in one launch: q norm + RoPE; on owner layers k/v
+        // norm, k RoPE and the append into the next cache row.
+        float *k_rows = nullptr, *v_rows = nullptr;
+        if (owner) {
+            rc = owner_rows(cache, layer, row_width, 1, &k_rows, &v_rows);
             if (rc != G4_OK) return rc;
         }
+        rc = prepare(ctx, q, owner ? k : nullptr, v, 1, position, hp->n_heads, hp->n_kv_heads, head_dim, q_norm_w,
+                     k_norm_w, hp->rms_norm_eps, pl.base, pl.factors, k_rows, v_rows, row_width, as_stream(stream));
+        if (rc != G4_OK) return rc;
+        if (owner) commit_rows(cache, layer, 1);
         // model.rs:407-408
         const float *keys = nullptr, *values = nullptr;
         int64_t stride = 0;
-        rc = g4_kv_view(cache, source, position + 1, &keys, &values, &stride);
+        rc = g4_kv_view(cache, pl.source, position + 1, &keys, &values, &stride);
         if (rc != G4_OK) return rc;
         int64_t begin = 0, end = position + 1;
-        if (!global) g4_windowed_len(position + 1, hp->sliding_window, &begin, &end);
-        if (stride != (int64_t)hp->n_kv_heads * head_dim)
+        if (!pl.global) g4_windowed_len(position + 1, hp->sliding_window, &begin, &end);
+        if (stride != row_width)
             return invalid("g4_layer_attention: source layer's row width differs from this layer's");
-        if (source_out) *source_out = source;
+        if (source_out) *source_out = pl.source;
         if (begin_out) *begin_out = begin;
         if (end_out) *end_out = end;
-        (void)st;
         // model.rs:409-410: q and k are RMS-normalised, so the scale is 1.0.
         return g4_attend_decode(ctx, q, keys, values, stride, begin, end, hp->n_heads,
                                 hp->n_kv_heads, head_dim, 1.0f, out, stream);
+    });
+}
+
+int g4_layer_prefill(g4_ctx *ctx, g4_kv_cache *cache, const g4_hparams *hp, int layer, int64_t pos0,
+                     int64_t n_tokens, float *q, float *k, float *v, const float *q_norm_w,
+                     const float *k_norm_w, const float *rope_freqs, float *out, int *source_out,
+                     g4_stream stream) {
+    return guarded([&] {
+        g4::clear_error();
+        if (!ctx || !cache || !hp) return invalid("g4_layer_prefill: null argument");
+        if (layer < 0 || layer >= hp->n_layers) return invalid("g4_layer_prefill: layer outside n_layers");
+        if (pos0 < 0 || n_tokens < 0) return invalid("g4_layer_prefill: negative position or token count");
+        LayerPlan pl;
+        int rc = plan_layer(hp, layer, rope_freqs, pl);
+        if (rc != G4_OK) return rc;
+        if (source_out) *source_out = pl.source;
+        if (n_tokens == 0) return (int)G4_OK;
+        // LocalWindowPolicy with no window attends nothing (eng/mod.rs:10-12).
+        if (!pl.global && hp->sliding_window <= 0)
+            return g4::set_error(G4_ERR_COMPUTE, "softmax input is not finite");
+        const int head_dim = pl.head_dim;
+        const int64_t row_width = (int64_t)hp->n_kv_heads * head_dim;
+        const bool owner = pl.source == layer;
+        float *k_rows = nullptr, *v_rows = nullptr;
+        if (owner) {
+            // Token pos0 appends its row, then views pos0 + 1 rows
+            // (model.rs:405-407): a cache shorter than pos0 fails there.
+            const int64_t have = layer < cache->n_layers ? cache->rows[layer] : 0;
+            if (have < pos0) return context_too_long(pos0 + 1, have + 1);
+            rc = owner_rows(cache, layer, row_width, n_tokens, &k_rows, &v_rows);
+            if (rc != G4_OK) return rc;
+        }
+        rc = prepare(ctx, q, owner ? k : nullptr, v, n_tokens, pos0, hp->n_heads, hp->n_kv_heads, head_dim,
+                     q_norm_w, k_norm_w, hp->rms_norm_eps, pl.base, pl.factors, k_rows, v_rows, row_width,
+                     as_stream(stream));
+        if (rc != G4_OK) return rc;
+        if (owner) commit_rows(cache, layer, n_tokens);
+        // The last token's view bounds every earlier one's.
+        const float *keys = nullptr, *values = nullptr;
+        int64_t stride = 0;
+        rc = g4_kv_view(cache, pl.source, pos0 + n_tokens, &keys, &values, &stride);
+        if (rc != G4_OK) return rc;
+        if (stride != row_width)
+            return invalid("g4_layer_prefill: source layer's row width differs from this layer's");
+        // Query i attends the rows a decode at position pos0 + i would
+        // (model.rs:407-410, eng/mod.rs:10-36), scale 1.0.
+        return g4_attend_prefill(ctx, q, keys, values, stride, pos0, n_tokens, pl.global ? 0 : hp->sliding_window,
+                                 hp->n_heads, hp->n_kv_heads, head_dim, 1.0f, out, stream);
     });
 }
 

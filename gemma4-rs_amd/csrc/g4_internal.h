@@ -95,6 +95,25 @@ int launch_rms_norm_rows(const float *x, int64_t n_rows, int64_t width, const fl
                          float *out, hipStream_t stream);
 int launch_rope_rows(float *x, int64_t n_tokens, int n_heads, int head_dim, int n_rot,
                      int64_t pos0, float theta_scale, const float *factors, hipStream_t stream);
+// Fused norm + RoPE + append of one layer step's q/k/v for n_tokens tokens
+// (token t at position pos0 + t).  q: [n_tokens][n_heads][head_dim]; k, v:
+// [n_tokens][n_kv_heads][head_dim] or k == nullptr (q only); k_rows/v_rows:
+// the cache rows of token 0 (row_stride floats apart) or nullptr.
+struct PrepareArgs {
+    float *q;
+    float *k;
+    float *v;
+    float *k_rows;
+    float *v_rows;
+    int64_t row_stride;
+    const float *q_w;
+    const float *k_w;
+    const float *factors;  // [head_dim/2] RoPE divisors or nullptr
+    int64_t n_tokens, pos0;
+    int n_heads, n_kv_heads, head_dim;
+    float eps, theta_scale;
+};
+int launch_prepare_qkv(const PrepareArgs &a, hipStream_t stream);
 int launch_matmul(const float *a, const float *b, int64_t m, int64_t n, int64_t k, float *out,
                   hipStream_t stream);
 int launch_softmax(const float *x, int64_t n, float *out, unsigned *status, hipStream_t stream);

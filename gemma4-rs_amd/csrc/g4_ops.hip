@@ -73,6 +73,103 @@ __global__ __launch_bounds__(256) void rope_rows_kernel(float *x, int n_heads, i
     }
 }
 
+// The attention inputs of one layer step, fused (model.rs:394-406): for each
+// token t at position pos0 + t, every q head gets norm_heads(attn_q_norm)
+// then rope_heads; on owner layers every k head gets norm_heads(attn_k_norm)
+// then rope_heads and every v head norm_heads(None).  Results go back in
+// place and, when cache rows are given, to row t of the K and V caches (the
+// `append` of model.rs:405).  One workgroup per token: the angle table of
+// the token's position is built once in LDS and serves its q and k heads;
+// each wavefront normalises one head at a time, stages it in LDS, then
+// rotates its NEOX pairs.  The arithmetic is that of rms_norm_rows_kernel
+// and rope_rows_kernel, operation for operation.
+constexpr int kPrepWaves = 4;
+constexpr int kPrepMaxDim = 1024;
+
+__global__ __launch_bounds__(64 * kPrepWaves) void prepare_qkv_kernel(PrepareArgs a) {
+#pragma clang fp contract(off)
+    __shared__ float theta[kPrepMaxDim / 2];
+    __shared__ float stage[kPrepWaves][kPrepMaxDim];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int d = a.head_dim, half = d / 2;
+    const int64_t t = blockIdx.x;
+    if (threadIdx.x == 0) {
+        float th = (float)(a.pos0 + t);
+        for (int i = 0; i < half; ++i) {
+            theta[i] = th;
+            th = th * a.theta_scale;
+        }
+    }
+    __syncthreads();
+    const int n_k = a.k ? a.n_kv_heads : 0;
+    const int rows = a.n_heads + 2 * n_k;
+    for (int r0 = 0; r0 < rows; r0 += kPrepWaves) {
+        const int r = r0 + wave;
+        const bool active = r < rows;
+        // Row r: q heads, then k heads, then v heads.
+        float *x = nullptr, *cache = nullptr;
+        const float *w = nullptr;
+        bool rope = true;
+        if (r < a.n_heads) {
+            x = a.q + (t * a.n_heads + r) * (int64_t)d;
+            w = a.q_w;
+        } else if (r < a.n_heads + n_k) {
+            const int h = r - a.n_heads;
+            x = a.k + (t * a.n_kv_heads + h) * (int64_t)d;
+            w = a.k_w;
+            if (a.k_rows) cache = a.k_rows + t * a.row_stride + (int64_t)h * d;
+        } else if (active) {
+            const int h = r - a.n_heads - n_k;
+            x = a.v + (t * a.n_kv_heads + h) * (int64_t)d;
+            rope = false;
+            if (a.v_rows) cache = a.v_rows + t * a.row_stride + (int64_t)h * d;
+        }
+        float scale = 0.0f;
+        if (active) {
+            double sum = 0.0;
+            for (int i = lane; i < d; i += 64) {
+                const float xv = x[i];
+                const float sq = xv * xv;
+                sum += (double)sq;
+            }
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+            const float mean = (float)(sum / (double)d);
+            const float root = (float)sqrt((double)(mean + a.eps));
+            scale = (float)(1.0 / (double)root);
+            for (int i = lane; i < d; i += 64) {
+                float y = x[i] * scale;
+                if (w) y = y * w[i];
+                if (rope) {
+                    stage[wave][i] = y;
+                } else {
+                    x[i] = y;
+                    if (cache) cache[i] = y;
+                }
+            }
+        }
+        __syncthreads();
+        if (active && rope) {
+            for (int i = lane; i < half; i += 64) {
+                const float factor = a.factors ? a.factors[i] : 1.0f;
+                const float angle = theta[i] / factor;
+                float sn, cs;
+                sincosf(angle, &sn, &cs);
+                const float p = stage[wave][i], q = stage[wave][i + half];
+                const float lo = p * cs - q * sn;
+                const float hi = p * sn + q * cs;
+                x[i] = lo;
+                x[i + half] = hi;
+                if (cache) {
+                    cache[i] = lo;
+                    cache[i + half] = hi;
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
 // matmul_f32 (ops.rs:9-39): row-major [m,k] x [k,n], sequential inner sum of
 // rounded products, as the reference's triple loop.
 __global__ void matmul_kernel(const float *a, const float *b, int64_t m, int64_t n, int64_t k,
@@ -150,6 +247,15 @@ int launch_rope_rows(float *x, int64_t n_tokens, int n_heads, int head_dim, int 
     hipLaunchKernelGGL(rope_rows_kernel, dim3((unsigned)n_tokens), dim3(256),
                        (size_t)(n_rot / 2) * sizeof(float), stream, x, n_heads, head_dim, n_rot,
                        pos0, theta_scale, factors);
+    G4_HIP(hipGetLastError());
+    return G4_OK;
+}
+
+int launch_prepare_qkv(const PrepareArgs &a, hipStream_t stream) {
+    if (a.n_tokens <= 0) return G4_OK;
+    if (a.head_dim > kPrepMaxDim)
+        return set_error(G4_ERR_COMPUTE, "head_dim above 1024 is not supported");
+    hipLaunchKernelGGL(prepare_qkv_kernel, dim3((unsigned)a.n_tokens), dim3(64 * kPrepWaves), 0, stream, a);
     G4_HIP(hipGetLastError());
     return G4_OK;
 }

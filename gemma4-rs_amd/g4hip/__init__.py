@@ -73,6 +73,10 @@ _SIGS = {
     "g4_kv_clear": (None, [c_vp]),
     "g4_layer_attention": (c_int, [c_vp, c_vp, c_vp, c_int, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                                    ctypes.POINTER(c_int), ctypes.POINTER(c_i64), ctypes.POINTER(c_i64), c_vp]),
+    "g4_prepare_qkv": (c_int, [c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_int, c_int, c_int, c_vp, c_vp, c_f32, c_f32,
+                               c_vp, c_vp, c_vp, c_i64, c_vp]),
+    "g4_layer_prefill": (c_int, [c_vp, c_vp, c_vp, c_int, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
+                                 ctypes.POINTER(c_int), c_vp]),
     "g4_layer_is_global": (c_int, [c_int, c_int]),
     "g4_kv_source_layer": (c_int, [c_int, c_int, c_int, ctypes.POINTER(c_int)]),
     "g4_windowed_len": (None, [c_i64, c_i64, ctypes.POINTER(c_i64), ctypes.POINTER(c_i64)]),
@@ -239,6 +243,13 @@ class Context:
         _raise(lib().g4_rope_neox_rows(self.handle, _ptr(x), n_tokens, n_heads, head_dim, n_rot, pos0, base,
                                        _ptr(freq_factors), nf, _stream(stream)))
 
+    def prepare_qkv(self, q, k, v, n_tokens, pos0, n_heads, n_kv_heads, head_dim, q_norm_w, k_norm_w, eps,
+                    rope_base, freq_factors=None, k_rows=None, v_rows=None, row_stride=0, stream=None):
+        """Fused q/k/v norm + RoPE (+ append into k_rows/v_rows), model.rs:394-406."""
+        _raise(lib().g4_prepare_qkv(self.handle, _ptr(q), _ptr(k), _ptr(v), n_tokens, pos0, n_heads, n_kv_heads,
+                                    head_dim, _ptr(q_norm_w), _ptr(k_norm_w), eps, rope_base, _ptr(freq_factors),
+                                    _ptr(k_rows), _ptr(v_rows), row_stride, _stream(stream)))
+
     # -- ComputePort -------------------------------------------------------
     def port_matmul(self, a, b, m, n, k, out, stream=None):
         _raise(lib().g4_port_matmul(self.handle, _ptr(a), _ptr(b), m, n, k, _ptr(out), _stream(stream)))
@@ -301,3 +312,12 @@ class KvCache:
                                         _ptr(out), ctypes.byref(src), ctypes.byref(b), ctypes.byref(e),
                                         _stream(stream)))
         return src.value, range(b.value, e.value)
+
+    def layer_prefill(self, hp, layer, pos0, n_tokens, q, k, v, q_norm_w, k_norm_w, rope_freqs, out, stream=None):
+        """The layer's attention segment for prompt positions pos0 .. pos0+n_tokens-1 in one
+        call (the token-at-a-time loop of generate.rs:37-41, batched); returns the source layer."""
+        src = c_int(0)
+        _raise(lib().g4_layer_prefill(self.ctx.handle, self.handle, ctypes.byref(hp), layer, pos0, n_tokens, _ptr(q),
+                                      _ptr(k), _ptr(v), _ptr(q_norm_w), _ptr(k_norm_w), _ptr(rope_freqs),
+                                      _ptr(out), ctypes.byref(src), _stream(stream)))
+        return src.value

@@ -167,6 +167,40 @@ int g4_layer_attention(g4_ctx *ctx, g4_kv_cache *cache, const g4_hparams *hp, in
                        const float *rope_freqs_dev, float *out_dev, int *source,
                        int64_t *kv_begin, int64_t *kv_end, g4_stream stream);
 
+/* The attention inputs of a layer step in one launch (model.rs:394-406):
+ * for token t of n_tokens, at position pos0 + t, norm_heads(q, q_norm_w)
+ * then rope_heads on q_dev [n_tokens][n_heads*head_dim]; when k_dev is not
+ * NULL also norm_heads(k, k_norm_w), norm_heads(v, none) and rope_heads on
+ * k, with k_dev/v_dev [n_tokens][n_kv_heads*head_dim].  Results are written
+ * in place and, when k_rows_dev/v_rows_dev are given, also to the cache rows
+ * k_rows_dev + t*row_stride (the append of model.rs:405).  RoPE rotates all
+ * head_dim dims with base rope_base; freq_factors_dev ([head_dim/2], may be
+ * NULL) divides the angles.  Norm weights may be NULL (no weight).  Same
+ * arithmetic as g4_rms_norm_rows followed by g4_rope_neox_rows. */
+int g4_prepare_qkv(g4_ctx *ctx, float *q_dev, float *k_dev, float *v_dev, int64_t n_tokens,
+                   int64_t pos0, int n_heads, int n_kv_heads, int head_dim,
+                   const float *q_norm_w_dev, const float *k_norm_w_dev, float eps,
+                   float rope_base, const float *freq_factors_dev, float *k_rows_dev,
+                   float *v_rows_dev, int64_t row_stride, g4_stream stream);
+
+/* Whole-layer prefill: the attention segment of Gemma4CpuModel::layer
+ * (model.rs:386-411) for the n_tokens prompt positions pos0, pos0+1, ... in
+ * one call.  Run over the layers in ascending order, it gives what the
+ * reference's token-at-a-time prompt loop (crates/llm-idea/src/transformer.rs:40-53,
+ * crates/llm-gemma4/src/impl_/generate.rs:37-41) computes: query i attends the
+ * rows a decode at position pos0+i would.  q_dev [n_tokens][n_heads*d] and,
+ * on owner layers, k_dev/v_dev [n_tokens][n_kv_heads*d] are prepared in place
+ * (as g4_prepare_qkv) and k/v appended; out_dev [n_tokens][n_heads*d].  An
+ * owner layer's cache must already hold pos0 rows (else ContextTooLong, as
+ * the first token's view would fail); a shared layer's source must hold
+ * pos0 + n_tokens rows.  The reference has no batched prefill; this is the
+ * driver its prompt loop would call. */
+int g4_layer_prefill(g4_ctx *ctx, g4_kv_cache *cache, const g4_hparams *hp, int layer,
+                     int64_t pos0, int64_t n_tokens, float *q_dev, float *k_dev, float *v_dev,
+                     const float *q_norm_w_dev, const float *k_norm_w_dev,
+                     const float *rope_freqs_dev, float *out_dev, int *source,
+                     g4_stream stream);
+
 /* ----------------------------------------------------------- policies */
 /* layer_attention_kind (idea/mod.rs:238-246): 1 global, 0 local. */
 int g4_layer_is_global(int n_layers, int layer);
