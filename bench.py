@@ -15,7 +15,8 @@ kernels' time to MI355X's 8 TB/s; `cpu_baseline` is the oracle (the C
 restatement of the reference's CPU attention, same `concat` copy and per-head
 thread pool) timed on this host's cores on a bounded sample of the same step.
 `workloads` carries the other measured shapes (sliding decode, the 35-layer
-stack, 2048-token prefill, the ragged 32-sequence batch).
+stack, 2048-token prefill, the ragged 32-sequence batch, the layer drivers with
+their fused input preparation).
 """
 import argparse
 import json
@@ -192,6 +193,59 @@ def bench_prefill(ctx, torch, prep, steps, warmup, N=2048):
     return res
 
 
+def bench_layer_steps(ctx, torch, prep, steps, warmup, T=4096, N=2048):
+    """The launches of the layer drivers, input preparation included: a
+    global-layer decode step (g4_layer_attention: fused q/k/v norm + RoPE +
+    append of row T-1, then attention over T rows) and a 2048-token prompt
+    through one sliding and one global layer (g4_layer_prefill: the fused
+    preparation of all N tokens with their appends, then the prefill).  The
+    cache rows written are the same each step, so the steps replay as a graph."""
+    res = {}
+    d = 512
+    freqs = prep.rope_freqs(d)
+    K = prep.rows(T, d, 0, GLOBAL_BASE, freqs)
+    V = prep.rows(T, d, 0, 0.0, None, rope=False)
+    q, k, v = prep.randn(N_HEADS * d), prep.randn(N_KV * d), prep.randn(N_KV * d)
+    wq, wk = torch.ones(d, device="cuda"), torch.ones(d, device="cuda")
+    out = torch.zeros(N_HEADS * d, device="cuda")
+    row = (T - 1) * N_KV * d
+
+    def step(i):
+        ctx.prepare_qkv(q, k, v, 1, T - 1, N_HEADS, N_KV, d, wq, wk, EPS, GLOBAL_BASE, freqs,
+                        k_rows=K.view(-1)[row:], v_rows=V.view(-1)[row:], row_stride=N_KV * d)
+        ctx.attend_decode(q, K, V, 0, T, N_HEADS, N_KV, d, out)
+
+    wall, ev = time_steps(torch, step, steps, warmup, block=20)
+    ctx.check_status()
+    res["decode_global_d512_ctx4096_layer_step"] = {"us_per_layer": ev / steps * 1e6,
+                                                    "wall_us_per_layer": wall / steps * 1e6,
+                                                    "note": "K/V resident (one copy): preparation + attention"}
+    del K, V
+    total_flops, total_s = 0, 0.0
+    psteps = max(5, steps // 20)
+    for name, d, window, base in (("sliding_d256_W512", 256, WINDOW, LOCAL_BASE), ("global_d512", 512, 0, GLOBAL_BASE)):
+        f = prep.rope_freqs(d) if not window else None
+        Kc = torch.zeros(N * N_KV * d, device="cuda")
+        Vc = torch.zeros(N * N_KV * d, device="cuda")
+        q, k, v = prep.randn(N * N_HEADS * d), prep.randn(N * N_KV * d), prep.randn(N * N_KV * d)
+        wq, wk = torch.ones(d, device="cuda"), torch.ones(d, device="cuda")
+        out = torch.zeros(N * N_HEADS * d, device="cuda")
+
+        def pstep(i):
+            ctx.prepare_qkv(q, k, v, N, 0, N_HEADS, N_KV, d, wq, wk, EPS, base, f, k_rows=Kc, v_rows=Vc,
+                            row_stride=N_KV * d)
+            ctx.attend_prefill(q, Kc, Vc, 0, N, window, N_HEADS, N_KV, d, out)
+
+        wall, ev = time_steps(torch, pstep, psteps, 2)
+        ctx.check_status()
+        fl = prefill_flops(N, window, d)
+        res[f"prefill_2048_{name}_layer"] = {"us": ev / psteps * 1e6, "tflops": fl / (ev / psteps) / 1e12}
+        total_flops += fl
+        total_s += ev / psteps
+    res["prefill_2048_both_layers_tflops_with_preparation"] = total_flops / total_s / 1e12
+    return res
+
+
 def bench_ragged(ctx, torch, prep, steps, warmup, B=32, seed=2024):
     import numpy as np
     lens = np.random.default_rng(seed).integers(1024, 32768 + 1, size=B).astype(np.int64)
@@ -279,7 +333,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-workloads", action="store_true", help="only the headline step")
-    ap.add_argument("--only", choices=["global", "sliding", "stack", "prefill", "ragged", "copy"],
+    ap.add_argument("--only", choices=["global", "sliding", "stack", "prefill", "ragged", "layer", "copy"],
                     help="run one workload alone (for profiling); prints its result.  'copy' is a "
                          "plain 256 MiB device copy, the reference point for HBM byte counters")
     args = ap.parse_args()
@@ -301,6 +355,7 @@ def main():
                   "stack": lambda: bench_stack(ctx, torch, prep, g4hip, k, 5),
                   "prefill": lambda: bench_prefill(ctx, torch, prep, max(5, k // 10), 2),
                   "ragged": lambda: bench_ragged(ctx, torch, prep, max(5, k // 4), 2),
+                  "layer": lambda: bench_layer_steps(ctx, torch, prep, args.steps, args.warmup),
                   "copy": lambda: bench_copy(torch, max(5, k // 4))}[args.only]
             res = fn()
             res.pop("host", None)
@@ -318,6 +373,7 @@ def main():
             workloads["e2b_stack_35_layers_ctx8192"] = bench_stack(ctx, torch, prep, g4hip, k, 5)
             workloads["prefill_2048"] = bench_prefill(ctx, torch, prep, max(5, k // 10), 2)
             workloads["ragged_decode_B32"] = bench_ragged(ctx, torch, prep, max(5, k // 4), 2)
+            workloads["layer_drivers"] = bench_layer_steps(ctx, torch, prep, args.steps, args.warmup)
         workloads["global_decode_d512_ctx4096_warm"] = {
             "us_per_layer": g["event_warm"] / args.steps * 1e6,
             "gbs": g["bytes"] / (g["event_warm"] / args.steps) / 1e9,

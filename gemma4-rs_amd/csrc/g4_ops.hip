@@ -1,6 +1,8 @@
 // Attention input preparation (per-head RMS norm, NEOX RoPE) and the
 // ComputePort method set on the device.  Citations: crates/llm-backend-cpu/src/ops.rs.
 
+#include <algorithm>
+
 #include "g4_internal.h"
 
 namespace g4 {
@@ -82,7 +84,8 @@ __global__ __launch_bounds__(256) void rope_rows_kernel(float *x, int n_heads, i
 // the token's position is built once in LDS and serves its q and k heads;
 // each wavefront normalises one head at a time, stages it in LDS, then
 // rotates its NEOX pairs.  The arithmetic is that of rms_norm_rows_kernel
-// and rope_rows_kernel, operation for operation.
+// and rope_rows_kernel, operation for operation.  This form serves any head
+// width up to 1024; prepare_heads_kernel below serves the common ones.
 constexpr int kPrepWaves = 4;
 constexpr int kPrepMaxDim = 1024;
 
@@ -167,6 +170,101 @@ __global__ __launch_bounds__(64 * kPrepWaves) void prepare_qkv_kernel(PrepareArg
             }
         }
         __syncthreads();
+    }
+}
+
+// The same preparation for head widths D that are multiples of 128: lane l
+// holds elements l + 64m of its head in registers, so NEOX partners (i,
+// i + D/2) sit in the same lane and a head needs one load, one reduction and
+// one store.  One wavefront per head row (up to 16 per workgroup, grid.y
+// covers more), all of a token's rows loaded at once; wave 0 builds the
+// angle table (the reference's sequential recurrence) while the loads are
+// in flight.
+constexpr int kPrepMaxRowsPerGroup = 16;
+
+template <int D>
+__global__ __launch_bounds__(64 * kPrepMaxRowsPerGroup) void prepare_heads_kernel(PrepareArgs a) {
+#pragma clang fp contract(off)
+    constexpr int E = D / 64, HALF = D / 2, PE = E / 2;  // elements and pairs per lane
+    __shared__ float theta[HALF];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t t = blockIdx.x;
+    const int n_k = a.k ? a.n_kv_heads : 0;
+    const int rows = a.n_heads + 2 * n_k;
+    const int r = blockIdx.y * kPrepMaxRowsPerGroup + wave;
+    const bool active = r < rows;
+    float *x = nullptr, *cache = nullptr;
+    const float *w = nullptr;
+    bool rope = true;
+    if (r < a.n_heads) {
+        x = a.q + (t * a.n_heads + r) * (int64_t)D;
+        w = a.q_w;
+    } else if (r < a.n_heads + n_k) {
+        const int h = r - a.n_heads;
+        x = a.k + (t * a.n_kv_heads + h) * (int64_t)D;
+        w = a.k_w;
+        if (a.k_rows) cache = a.k_rows + t * a.row_stride + (int64_t)h * D;
+    } else if (active) {
+        const int h = r - a.n_heads - n_k;
+        x = a.v + (t * a.n_kv_heads + h) * (int64_t)D;
+        w = nullptr;
+        rope = false;
+        if (a.v_rows) cache = a.v_rows + t * a.row_stride + (int64_t)h * D;
+    }
+    float xv[E], wv[E], fv[PE];
+    if (active) {
+#pragma unroll
+        for (int m = 0; m < E; ++m) xv[m] = x[lane + 64 * m];
+        if (w) {
+#pragma unroll
+            for (int m = 0; m < E; ++m) wv[m] = w[lane + 64 * m];
+        }
+        if (rope) {
+#pragma unroll
+            for (int m = 0; m < PE; ++m) fv[m] = a.factors ? a.factors[lane + 64 * m] : 1.0f;
+        }
+    }
+    if (threadIdx.x == 0) {
+        float th = (float)(a.pos0 + t);
+        for (int i = 0; i < HALF; ++i) {
+            theta[i] = th;
+            th = th * a.theta_scale;
+        }
+    }
+    __syncthreads();
+    if (!active) return;
+    double sum = 0.0;
+#pragma unroll
+    for (int m = 0; m < E; ++m) {
+        const float sq = xv[m] * xv[m];
+        sum += (double)sq;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+    const float mean = (float)(sum / (double)D);
+    const float root = (float)sqrt((double)(mean + a.eps));
+    const float scale = (float)(1.0 / (double)root);
+#pragma unroll
+    for (int m = 0; m < E; ++m) {
+        xv[m] = xv[m] * scale;
+        if (w) xv[m] = xv[m] * wv[m];
+    }
+    if (rope) {
+#pragma unroll
+        for (int m = 0; m < PE; ++m) {
+            const float angle = theta[lane + 64 * m] / fv[m];
+            float sn, cs;
+            sincosf(angle, &sn, &cs);
+            const float p = xv[m], q = xv[m + PE];
+            xv[m] = p * cs - q * sn;
+            xv[m + PE] = p * sn + q * cs;
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < E; ++m) x[lane + 64 * m] = xv[m];
+    if (cache) {
+#pragma unroll
+        for (int m = 0; m < E; ++m) cache[lane + 64 * m] = xv[m];
     }
 }
 
@@ -255,7 +353,17 @@ int launch_prepare_qkv(const PrepareArgs &a, hipStream_t stream) {
     if (a.n_tokens <= 0) return G4_OK;
     if (a.head_dim > kPrepMaxDim)
         return set_error(G4_ERR_COMPUTE, "head_dim above 1024 is not supported");
-    hipLaunchKernelGGL(prepare_qkv_kernel, dim3((unsigned)a.n_tokens), dim3(64 * kPrepWaves), 0, stream, a);
+    const int rows = a.n_heads + (a.k ? 2 * a.n_kv_heads : 0);
+    const dim3 fgrid((unsigned)a.n_tokens, (unsigned)((rows + kPrepMaxRowsPerGroup - 1) / kPrepMaxRowsPerGroup));
+    const dim3 fblock(64 * (unsigned)std::min(rows, kPrepMaxRowsPerGroup));
+    switch (a.head_dim) {
+    case 128: hipLaunchKernelGGL(prepare_heads_kernel<128>, fgrid, fblock, 0, stream, a); break;
+    case 256: hipLaunchKernelGGL(prepare_heads_kernel<256>, fgrid, fblock, 0, stream, a); break;
+    case 512: hipLaunchKernelGGL(prepare_heads_kernel<512>, fgrid, fblock, 0, stream, a); break;
+    case 1024: hipLaunchKernelGGL(prepare_heads_kernel<1024>, fgrid, fblock, 0, stream, a); break;
+    default:
+        hipLaunchKernelGGL(prepare_qkv_kernel, dim3((unsigned)a.n_tokens), dim3(64 * kPrepWaves), 0, stream, a);
+    }
     G4_HIP(hipGetLastError());
     return G4_OK;
 }

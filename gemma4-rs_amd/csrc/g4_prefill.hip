@@ -435,39 +435,64 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillK p) {
 
 constexpr int kPrefillMaxUnits = kPrefillMaxUnitsDev;  // per position block
 
-// Per-context cache of the unit table for the last prefill shape.
+// A unit table in device memory, for one prefill shape.
 struct PrefillPlan {
     int64_t pos0 = -1, N = -1, window = -1;
     int unit_tiles = 0;
     int n_units = 0, n_blocks = 0, n_slots = 0;
     PrefillUnit *units = nullptr;
     PrefillBlockInfo *blocks = nullptr;
-    size_t cap_units = 0, cap_blocks = 0;
+    uint64_t last_use = 0;
 };
+
+// The context's tables for the last few shapes (a layer-by-layer prompt
+// alternates sliding and global shapes).  A cached table is never written
+// again, so kernels still in flight on any stream keep reading a valid
+// table; only evicting one waits for the device.
+constexpr size_t kPrefillPlans = 8;
+struct PrefillPlans {
+    std::vector<PrefillPlan> plans;
+    uint64_t tick = 0;
+};
+
+void free_plan(PrefillPlan &pl) {
+    if (pl.units) (void)hipFree(pl.units);
+    if (pl.blocks) (void)hipFree(pl.blocks);
+    pl.units = nullptr;
+    pl.blocks = nullptr;
+}
 
 }  // namespace
 
-// The plan lives with the context (one per device; prefill calls on one
+// The tables live with the context (one per device; prefill calls on one
 // context are issued from one host thread).
-static PrefillPlan &plan_of(g4_ctx *ctx) {
-    if (!ctx->prefill_plan) ctx->prefill_plan = new PrefillPlan();
-    return *static_cast<PrefillPlan *>(ctx->prefill_plan);
+static PrefillPlans &plans_of(g4_ctx *ctx) {
+    if (!ctx->prefill_plan) ctx->prefill_plan = new PrefillPlans();
+    return *static_cast<PrefillPlans *>(ctx->prefill_plan);
 }
 
 void release_prefill_plan(g4_ctx *ctx) {
     if (!ctx->prefill_plan) return;
-    auto *pl = static_cast<PrefillPlan *>(ctx->prefill_plan);
-    if (pl->units) (void)hipFree(pl->units);
-    if (pl->blocks) (void)hipFree(pl->blocks);
-    delete pl;
+    auto *ps = static_cast<PrefillPlans *>(ctx->prefill_plan);
+    for (auto &pl : ps->plans) free_plan(pl);
+    delete ps;
     ctx->prefill_plan = nullptr;
 }
 
-static int build_plan(g4_ctx *ctx, const PrefillArgs &a, PrefillPlan &pl) {
+// The unit table of a's shape: cached, or built and uploaded (synchronously:
+// graph capture needs an earlier call with the same shape).
+static int plan_for(g4_ctx *ctx, const PrefillArgs &a, const PrefillPlan **out) {
     // Longest unit: 32 tiles (512 keys) on 512-wide heads, 64 on 256-wide
     // ones (a 512-key window then needs no merge).
     const int unit_tiles = a.head_dim > 256 ? 32 : 64;
-    if (pl.pos0 == a.pos0 && pl.N == a.N && pl.window == a.window && pl.unit_tiles == unit_tiles) return G4_OK;
+    PrefillPlans &ps = plans_of(ctx);
+    ++ps.tick;
+    for (auto &pl : ps.plans)
+        if (pl.pos0 == a.pos0 && pl.N == a.N && pl.window == a.window && pl.unit_tiles == unit_tiles) {
+            pl.last_use = ps.tick;
+            *out = &pl;
+            return G4_OK;
+        }
     const int n_blocks = (int)((a.N + kPosPerBlock - 1) / kPosPerBlock);
     std::vector<PrefillUnit> units;
     std::vector<PrefillBlockInfo> blocks(n_blocks);
@@ -492,22 +517,7 @@ static int build_plan(g4_ctx *ctx, const PrefillArgs &a, PrefillPlan &pl) {
     std::stable_sort(units.begin(), units.end(), [](const PrefillUnit &x, const PrefillUnit &y) {
         return (x.t_hi - x.t_lo) > (y.t_hi - y.t_lo);
     });
-    if (units.size() > pl.cap_units) {
-        if (pl.units) G4_HIP(hipFree(pl.units));
-        pl.units = nullptr;
-        G4_HIP(hipMalloc(&pl.units, units.size() * sizeof(PrefillUnit)));
-        pl.cap_units = units.size();
-    }
-    if (blocks.size() > pl.cap_blocks) {
-        if (pl.blocks) G4_HIP(hipFree(pl.blocks));
-        pl.blocks = nullptr;
-        G4_HIP(hipMalloc(&pl.blocks, blocks.size() * sizeof(PrefillBlockInfo)));
-        pl.cap_blocks = blocks.size();
-    }
-    // A new shape uploads its table synchronously (graph capture needs a
-    // previous call with the same shape).
-    G4_HIP(hipMemcpy(pl.units, units.data(), units.size() * sizeof(PrefillUnit), hipMemcpyHostToDevice));
-    G4_HIP(hipMemcpy(pl.blocks, blocks.data(), blocks.size() * sizeof(PrefillBlockInfo), hipMemcpyHostToDevice));
+    PrefillPlan pl;
     pl.pos0 = a.pos0;
     pl.N = a.N;
     pl.window = a.window;
@@ -515,6 +525,30 @@ static int build_plan(g4_ctx *ctx, const PrefillArgs &a, PrefillPlan &pl) {
     pl.n_units = (int)units.size();
     pl.n_blocks = n_blocks;
     pl.n_slots = n_slots;
+    pl.last_use = ps.tick;
+    hipError_t e = hipMalloc(&pl.units, units.size() * sizeof(PrefillUnit));
+    if (e == hipSuccess) e = hipMalloc(&pl.blocks, blocks.size() * sizeof(PrefillBlockInfo));
+    if (e == hipSuccess)
+        e = hipMemcpy(pl.units, units.data(), units.size() * sizeof(PrefillUnit), hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+        e = hipMemcpy(pl.blocks, blocks.data(), blocks.size() * sizeof(PrefillBlockInfo), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        free_plan(pl);
+        return hip_failed(e, "prefill unit table");
+    }
+    if (ps.plans.size() >= kPrefillPlans) {
+        size_t lru = 0;
+        for (size_t i = 1; i < ps.plans.size(); ++i)
+            if (ps.plans[i].last_use < ps.plans[lru].last_use) lru = i;
+        // Kernels on any stream may still read the evicted table.
+        G4_HIP(hipDeviceSynchronize());
+        free_plan(ps.plans[lru]);
+        ps.plans[lru] = pl;
+        *out = &ps.plans[lru];
+    } else {
+        ps.plans.push_back(pl);
+        *out = &ps.plans.back();
+    }
     return G4_OK;
 }
 
@@ -543,9 +577,10 @@ int launch_prefill(g4_ctx *ctx, const PrefillArgs &a, hipStream_t stream) {
         d.out = a.out;
         return launch_decode(ctx, d, stream);
     }
-    PrefillPlan &pl = plan_of(ctx);
-    int rc = build_plan(ctx, a, pl);
+    const PrefillPlan *plp = nullptr;
+    int rc = plan_for(ctx, a, &plp);
     if (rc != G4_OK) return rc;
+    const PrefillPlan &pl = *plp;
     PrefillK p{};
     p.q = a.q;
     p.k = a.k;
