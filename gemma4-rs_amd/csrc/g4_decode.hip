@@ -307,7 +307,8 @@ struct DecodeAcc {
     // score chains, the cross-wave sum, the softmax bookkeeping and the P.V
     // chains of a pair run together, so each fixed latency -- the barrier,
     // the LDS round trip, the softmax's dependent steps -- is paid once per
-    // 32 keys.
+    // 32 keys.  NT = 1: only the first tile (a split of at most 16 keys).
+    template <int NT = 2>
     __device__ __forceinline__ void pair(const L &ln, const KvTile<D> (&P)[2], int valid, float scale,
                                          PairScores<D> &sx, int &buf) {
         // Partial S^T of both tiles over this wave's dims (two MFMA chains).
@@ -317,17 +318,18 @@ struct DecodeAcc {
 #pragma unroll
             for (int j = 0; j < 4; ++j)
 #pragma unroll
-                for (int t = 0; t < 2; ++t)
+                for (int t = 0; t < NT; ++t)
                     acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(P[t].k[u][j], qreg[u][j], acc[t], 0, 0, 0);
 
         // The tiles' S^T: the waves' partials summed in a fixed order, so
         // every wave holds the same bits (all reads issue before the first add).
-        sx[buf][0][ln.wave][ln.lane] = acc[0];
-        sx[buf][1][ln.wave][ln.lane] = acc[1];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) sx[buf][t][ln.wave][ln.lane] = acc[t];
         __syncthreads();
         f32x4 sc[2];
+        if constexpr (NT == 1) sc[1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
+        for (int t = 0; t < NT; ++t) {
             f32x4 v[NW];
 #pragma unroll
             for (int w = 0; w < NW; ++w) v[w] = sx[buf][t][w][ln.lane];
@@ -346,9 +348,9 @@ struct DecodeAcc {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 sv[4 * t + r] = sc[t][r] * scale;
-                bad |= __builtin_amdgcn_classf(sv[4 * t + r], 0x203);  // signalling/quiet NaN, +inf
+                if (t < NT) bad |= __builtin_amdgcn_classf(sv[4 * t + r], 0x203);  // signalling/quiet NaN, +inf
             }
-        if (valid < 32) {
+        if (NT == 1 || valid < 32) {
 #pragma unroll
             for (int k = 0; k < 8; ++k)
                 if (16 * (k >> 2) + 4 * ln.g + (k & 3) >= valid) sv[k] = -INFINITY;
@@ -373,7 +375,7 @@ struct DecodeAcc {
         // O^T += V^T . P^T: k-step (t, r) covers key 16t + 4g + r; O^T tile i
         // holds dims base + TW*c' + i for output row c'.
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+        for (int t = 0; t < NT; ++t)
 #pragma unroll
             for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -421,6 +423,11 @@ __device__ __forceinline__ void run_pairs(const DecodeLane<D> &ln, DecodeAcc<D> 
                                           float scale, PairScores<D> &sx, int &buf) {
     constexpr int NPAIR = NBUF / 2;
     KvTile<D> T[NPAIR][2];
+    if (n_keys - 32 * q_first <= 16) {  // a single tile: its second half is not computed
+        ln.load_tile(krs, vrs, 2 * q_first, T[0][0]);
+        acc.template pair<1>(ln, T[0], n_keys - 32 * q_first, scale, sx, buf);
+        return;
+    }
     auto load_pair = [&](int i, KvTile<D> (&P)[2]) {
         const int q = q_first + (i < n_pairs ? i : n_pairs - 1);
         ln.load_tile(krs, vrs, 2 * q, P[0]);
@@ -805,18 +812,20 @@ int launch_mode(g4_ctx *ctx, const DecodeArgs &a, DecodeK p, hipStream_t stream)
         return launch_stream(ctx, a, p, stream);
 
     // Split-K sizing.  A split is a power of two of at least one 16-key
-    // MFMA tile.  One sequence: about two workgroups per CU, at least 32
-    // keys each (a split's fixed cost -- its first loads and its partial --
-    // outweighs a smaller share).  Ragged batches: about eight per CU, so
-    // that sequences of very different lengths still balance over the CUs.
-    // Contexts of a few tiles run as one split (no merge).
+    // MFMA tile.  One sequence: one workgroup per CU (the occupancy of the
+    // split kernel), down to a single tile each -- a workgroup's time is
+    // its MFMA and softmax work, so spreading the tiles over every CU wins
+    // over fewer, longer splits.  Ragged batches: about eight per CU, at
+    // least 64 keys, so that sequences of very different lengths still
+    // balance over the CUs.  Contexts of a few tiles run as one split (no
+    // merge).
     const int64_t units = (int64_t)a.B * a.n_kv_heads;
     const int64_t max_len = a.max_kv_len > 0 ? a.max_kv_len : 1;
     int64_t chunk = ctx->decode_chunk;
     if (chunk <= 0) {
-        const int64_t target = (MODE == kSingle ? 2LL : 8LL) * ctx->num_cus;
+        const int64_t target = (MODE == kSingle ? 1LL : 8LL) * ctx->num_cus;
         chunk = (max_len * units + target - 1) / target;
-        const int64_t floor_keys = MODE == kSingle ? 32 : 64;
+        const int64_t floor_keys = MODE == kSingle ? 16 : 64;
         if (chunk < floor_keys) chunk = floor_keys;
         if (max_len <= 64) chunk = max_len;
     }
