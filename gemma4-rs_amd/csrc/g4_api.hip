@@ -1,6 +1,7 @@
 // C ABI entry points: context, errors, attention calls, device KvCache, the
 // layer attention driver, the engine's policies and the ComputePort methods.
 
+#include <climits>
 #include <math.h>
 #include <new>
 #include <string>
@@ -669,6 +670,139 @@ int g4_layer_prefill(g4_ctx *ctx, g4_kv_cache *cache, const g4_hparams *hp, int 
         // (model.rs:407-410, eng/mod.rs:10-36), scale 1.0.
         return g4_attend_prefill(ctx, q, keys, values, stride, pos0, n_tokens, pl.global ? 0 : hp->sliding_window,
                                  hp->n_heads, hp->n_kv_heads, head_dim, 1.0f, out, stream);
+    });
+}
+
+// ------------------------------------------------------------------ mat-vecs
+namespace {
+
+// matvec.rs:206-214 (check_shape) with the reference's message.
+int check_weight_shape(const char *kind, int64_t len, int64_t rows, int64_t row_len) {
+    if (len >= 0 && rows >= 0 && row_len >= 0 && (row_len == 0 || rows <= INT64_MAX / row_len) &&
+        rows * row_len == len)
+        return G4_OK;
+    return g4::set_error(G4_ERR_COMPUTE, std::string(kind) + " weight has " + std::to_string(len) +
+                                             " elements, expected " + std::to_string(rows) + " rows of " +
+                                             std::to_string(row_len));
+}
+
+int q8_cols_error(const char *what, int64_t cols) {
+    return g4::set_error(G4_ERR_COMPUTE, std::string("Q8_0 ") + what + " " + std::to_string(cols) +
+                                             " is not a multiple of 32");
+}
+
+// The Q8_0-activation forms: matvec, softcap, geglu.
+int q8_matvec(g4_ctx *ctx, g4::MatvecKind kind, const uint8_t *w, const uint8_t *w2, int64_t w_bytes, int64_t rows,
+              int64_t cols, const float *xs, const int8_t *xq, float arg, float *out, g4_stream stream) {
+    if (!ctx) return invalid("mat-vec: null context");
+    if (cols < 0 || cols % 32 != 0) return q8_cols_error("activation length", cols);
+    const int rc = check_weight_shape("Q8_0", w_bytes, rows, cols / 32 * 34);
+    if (rc != G4_OK) return rc;
+    g4::MatvecArgs a{};
+    a.kind = kind;
+    a.w = w;
+    a.w2 = w2;
+    a.rows = rows;
+    a.cols = cols;
+    a.xs = xs;
+    a.xq = (const signed char *)xq;
+    a.arg = arg;
+    a.out = out;
+    return g4::launch_matvec(ctx, a, as_stream(stream));
+}
+
+}  // namespace
+
+int g4_quantize_q8_0(g4_ctx *ctx, const float *x, int64_t n, float *scales, int8_t *quants, g4_stream stream) {
+    return guarded([&] {
+        g4::clear_error();
+        if (!ctx) return invalid("g4_quantize_q8_0: null context");
+        // matvec.rs:36-42
+        if (n < 0 || n % 32 != 0) return q8_cols_error("activation length", n);
+        return g4::launch_quantize_q8_0(x, n, scales, (signed char *)quants, as_stream(stream));
+    });
+}
+
+int g4_matvec_q8_0(g4_ctx *ctx, const uint8_t *w, int64_t w_bytes, int64_t rows, int64_t cols,
+                   const float *x_scales, const int8_t *x_quants, float *out, g4_stream stream) {
+    return guarded([&] {
+        g4::clear_error();
+        return q8_matvec(ctx, g4::MatvecKind::Q8, w, nullptr, w_bytes, rows, cols, x_scales, x_quants, 0.0f, out,
+                         stream);
+    });
+}
+
+int g4_matvec_q8_0_softcap(g4_ctx *ctx, const uint8_t *w, int64_t w_bytes, int64_t rows, int64_t cols,
+                           const float *x_scales, const int8_t *x_quants, float cap, float *out, g4_stream stream) {
+    return guarded([&] {
+        g4::clear_error();
+        return q8_matvec(ctx, g4::MatvecKind::Q8Softcap, w, nullptr, w_bytes, rows, cols, x_scales, x_quants, cap,
+                         out, stream);
+    });
+}
+
+int g4_geglu_q8_0(g4_ctx *ctx, const uint8_t *gate, const uint8_t *up, int64_t w_bytes, int64_t rows, int64_t cols,
+                  const float *x_scales, const int8_t *x_quants, int fp16_gelu, float *out, g4_stream stream) {
+    return guarded([&] {
+        g4::clear_error();
+        return q8_matvec(ctx, fp16_gelu ? g4::MatvecKind::Q8GegluFp16 : g4::MatvecKind::Q8Geglu, gate, up, w_bytes,
+                         rows, cols, x_scales, x_quants, 0.0f, out, stream);
+    });
+}
+
+int g4_matvec_q8_0_f32(g4_ctx *ctx, const uint8_t *w, int64_t w_bytes, int64_t rows, int64_t cols, const float *x,
+                       int f64_sums, float *out, g4_stream stream) {
+    return guarded([&] {
+        g4::clear_error();
+        if (!ctx) return invalid("g4_matvec_q8_0_f32: null context");
+        // matvec.rs:186-190
+        if (cols < 0 || cols % 32 != 0) return q8_cols_error("row length", cols);
+        const int rc = check_weight_shape("Q8_0", w_bytes, rows, cols / 32 * 34);
+        if (rc != G4_OK) return rc;
+        g4::MatvecArgs a{};
+        a.kind = f64_sums ? g4::MatvecKind::Q8F64 : g4::MatvecKind::Q8F32;
+        a.w = w;
+        a.rows = rows;
+        a.cols = cols;
+        a.x = x;
+        a.out = out;
+        return g4::launch_matvec(ctx, a, as_stream(stream));
+    });
+}
+
+int g4_matvec_bf16(g4_ctx *ctx, const uint16_t *w, int64_t w_len, int64_t rows, int64_t cols, const float *x,
+                   float *out, g4_stream stream) {
+    return guarded([&] {
+        g4::clear_error();
+        if (!ctx) return invalid("g4_matvec_bf16: null context");
+        const int rc = check_weight_shape("BF16", w_len, rows, cols);
+        if (rc != G4_OK) return rc;
+        g4::MatvecArgs a{};
+        a.kind = g4::MatvecKind::Bf16;
+        a.w = (const unsigned char *)w;
+        a.rows = rows;
+        a.cols = cols;
+        a.x = x;
+        a.out = out;
+        return g4::launch_matvec(ctx, a, as_stream(stream));
+    });
+}
+
+int g4_matvec_f32(g4_ctx *ctx, const float *w, int64_t w_len, int64_t rows, int64_t cols, const float *x, float *out,
+                  g4_stream stream) {
+    return guarded([&] {
+        g4::clear_error();
+        if (!ctx) return invalid("g4_matvec_f32: null context");
+        const int rc = check_weight_shape("f32", w_len, rows, cols);
+        if (rc != G4_OK) return rc;
+        g4::MatvecArgs a{};
+        a.kind = g4::MatvecKind::F32;
+        a.w = (const unsigned char *)w;
+        a.rows = rows;
+        a.cols = cols;
+        a.x = x;
+        a.out = out;
+        return g4::launch_matvec(ctx, a, as_stream(stream));
     });
 }
 

@@ -116,6 +116,22 @@ struct PrepareArgs {
 int launch_prepare_qkv(const PrepareArgs &a, hipStream_t stream);
 int launch_matmul(const float *a, const float *b, int64_t m, int64_t n, int64_t k, float *out,
                   hipStream_t stream);
+
+// Mat-vecs over GGUF weight formats (g4_matvec.hip).
+enum class MatvecKind { Q8, Q8Softcap, Q8Geglu, Q8GegluFp16, Q8F32, Q8F64, Bf16, F32 };
+struct MatvecArgs {
+    MatvecKind kind;
+    const unsigned char *w;   // Q8_0 bytes, bf16 or f32 values, row-major [rows][cols]
+    const unsigned char *w2;  // the up matrix of the Geglu kinds
+    int64_t rows, cols;
+    const float *xs;          // Q8_0 activation: block scales [cols/32]
+    const signed char *xq;    // Q8_0 activation: values [cols]
+    const float *x;           // f32 activation [cols] (Q8F32, Q8F64, Bf16, F32)
+    float arg;                // soft-cap
+    float *out;               // [rows]
+};
+int launch_quantize_q8_0(const float *x, int64_t n, float *scales, signed char *quants, hipStream_t stream);
+int launch_matvec(g4_ctx *ctx, const MatvecArgs &a, hipStream_t stream);
 int launch_softmax(const float *x, int64_t n, float *out, unsigned *status, hipStream_t stream);
 int launch_add(const float *a, const float *b, int64_t n, float *out, hipStream_t stream);
 

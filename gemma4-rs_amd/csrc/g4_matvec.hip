@@ -1,0 +1,386 @@
+// Mat-vecs over the GGUF weight formats the engine keeps (Q8_0, BF16, F32)
+// and the activations fused into them (Gemma's GELU-gated FFN input, the
+// logit soft-cap): crates/llm-backend-cpu/src/matvec.rs, ops.rs:79-103.
+//
+// Every kernel reproduces the reference's arithmetic exactly: the integer
+// block dots are exact in any order, and every floating-point sum is taken
+// in the reference's order -- a row's block products (Q8_0) or element
+// products (BF16, F32, dequantized Q8_0) added one after another from -0.0,
+// as Rust's `Iterator::sum` does.  Only tanh inside GELU and the soft-cap
+// comes from the device's libm.
+//
+// Q8_0 with quantized activations (the engine's default numerics) is the
+// HBM-bound hot path: a wavefront takes whole rows, streams each row's bytes
+// into LDS with 16-byte loads (rows of 34-byte blocks are 16-byte aligned
+// when cols is a multiple of 256), and lane b then takes block b: its f16
+// scale and 32 int8 values against the activation's block b (held in the
+// lane's registers for the whole kernel), 8 v_dot4 steps.  The block
+// products are then summed in order by reading them lane by lane.  The
+// other formats, which the engine uses only for small tensors or for its
+// comparison numerics, give each lane one row and sum sequentially.
+
+#include <algorithm>
+#include <type_traits>
+
+#include "g4_internal.h"
+
+namespace g4 {
+namespace {
+
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kQ8Values = 32;  // values per Q8_0 block
+constexpr int kQ8Bytes = 34;   // f16 scale + 32 int8
+// Buffer resource (V#) word 3 for raw buffers on gfx950.
+constexpr int kBufferWord3 = 0x00020000;
+constexpr int kVmcntZero = 0x0F70;  // s_waitcnt vmcnt(0), other counters untouched
+
+// One 16-byte load per active lane from `rsrc` at byte offset voff, written
+// straight to LDS at lds + 16 * lane (lds is the same for the whole wavefront).
+__device__ inline void load_to_lds(__amdgpu_buffer_rsrc_t rsrc, u32x4 *lds, uint32_t voff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void *)lds, 16, voff, 0, 0, 0);
+#endif
+}
+
+__device__ inline float half_bits_to_float(unsigned bits) {
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)(bits & 0xffffu));
+}
+
+__device__ inline float round_to_half(float x) { return (float)(_Float16)x; }
+
+// Rust's `f32 as i8`: saturating, NaN -> 0.
+__device__ inline int saturate_i8(float v) {
+    if (v != v) return 0;
+    return (int)fminf(fmaxf(v, -128.0f), 127.0f);
+}
+
+// ops.rs:85-89, evaluated left to right as rustc does (no contraction).
+__device__ inline float gelu_tanh(float x) {
+#pragma clang fp contract(off)
+    return 0.5f * x * (1.0f + tanhf(0.7978846f * x * (1.0f + 0.044715f * x * x)));
+}
+
+// ops.rs:95-103
+__device__ inline float gelu_tanh_fp16_table(float x) {
+    if (x <= -10.0f) return 0.0f;
+    if (x >= 10.0f) return x;
+    return round_to_half(gelu_tanh(round_to_half(x)));
+}
+
+// quantize_q8_0 (matvec.rs:35-53): 32 lanes per block; max |x| over the
+// block (NaN ignored, as f32::max does), scale = max/127 kept as its f16
+// rounding, values x * (1/scale) rounded half to even and saturated.
+__global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *x, int64_t n, float *scales,
+                                                            signed char *quants) {
+#pragma clang fp contract(off)
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const float v = i < n ? x[i] : 0.0f;
+    float m = fmaxf(0.0f, fabsf(v));
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 32));
+    const float scale = m / 127.0f;
+    const float inverse = scale == 0.0f ? 0.0f : 1.0f / scale;
+    if (i >= n) return;
+    if ((i & 31) == 0) scales[i >> 5] = round_to_half(scale);
+    quants[i] = (signed char)saturate_i8(rintf(v * inverse));
+}
+
+// Epilogues of the Q8_0 row kernel.
+enum Epilogue : int { kPlain = 0, kSoftcap = 1, kGeglu = 2, kGegluFp16 = 3 };
+
+// W @ x for Q8_0 rows against a Q8_0 activation (matvec.rs:55-102).
+// NS = activation blocks per lane (blocks b = lane + 64 s).  Each wavefront
+// handles `rpw` consecutive rows, all loaded into its LDS area before any is
+// used; kGeglu* read a second matrix (up) beside the first (gate).
+template <int EPI, int NS>
+__global__ __launch_bounds__(256) void matvec_q8_0_kernel(const unsigned char *__restrict__ w,
+                                                          const unsigned char *__restrict__ w2, int64_t rows,
+                                                          int nb, const float *__restrict__ xs,
+                                                          const int *__restrict__ xq, float arg, int rpw,
+                                                          float *__restrict__ out) {
+#pragma clang fp contract(off)
+    extern __shared__ u32x4 stage[];
+    constexpr int NM = EPI >= kGeglu ? 2 : 1;  // matrices read
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row_len = nb * kQ8Bytes;  // bytes, a multiple of 16
+    const int chunks = row_len >> 4;    // 16-byte chunks per row
+    u32x4 *my = stage + (size_t)wave * rpw * NM * chunks;
+
+    // This lane's activation blocks: 8 packed int8 dwords and the scale.
+    int xqr[NS][8];
+    float xsr[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        const int b = lane + 64 * s;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xqr[s][j] = b < nb ? xq[b * 8 + j] : 0;
+        xsr[s] = b < nb ? xs[b] : 0.0f;
+    }
+
+    const int64_t row0 = ((int64_t)blockIdx.x * 4 + wave) * rpw;
+    // Stage rpw rows (of each matrix) in LDS with direct-to-LDS loads, all
+    // issued before any is waited for; rows past the end are not read.
+    for (int m = 0; m < NM; ++m) {
+        const unsigned char *src = m == 0 ? w : w2;
+        for (int r = 0; r < rpw; ++r) {
+            const int64_t row = row0 + r;
+            if (row >= rows) break;
+            const __amdgpu_buffer_rsrc_t rs =
+                __builtin_amdgcn_make_buffer_rsrc((void *)(src + row * row_len), 0, row_len, kBufferWord3);
+            u32x4 *dst = my + (r * NM + m) * chunks;
+            for (int k = 0; k * 64 < chunks; ++k)
+                if (k * 64 + lane < chunks) load_to_lds(rs, dst + 64 * k, (uint32_t)(k * 64 + lane) * 16u);
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(kVmcntZero);
+    __syncthreads();
+
+    for (int r = 0; r < rpw; ++r) {
+        const int64_t row = row0 + r;
+        if (row >= rows) break;
+        float acc[NM];
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+            const unsigned *rw = (const unsigned *)(my + (r * NM + m) * chunks);
+            float prod[NS];
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                const int b = lane + 64 * s;
+                prod[s] = 0.0f;
+                if (b < nb) {
+                    // Block b starts at byte 34b: dword 17(b/2), offset 0
+                    // (even b: scale in the low half, values from byte 2)
+                    // or dword 17(b/2) + 8, offset 2 (odd b: scale in the
+                    // high half, values dword-aligned after it).
+                    const unsigned *d = rw + 17 * (b >> 1) + ((b & 1) ? 8 : 0);
+                    unsigned raw[9];
+#pragma unroll
+                    for (int j = 0; j < 9; ++j) raw[j] = d[j];
+                    int dot = 0;
+                    float ws;
+                    if (b & 1) {
+                        ws = half_bits_to_float(raw[0] >> 16);
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) dot = __builtin_amdgcn_sdot4((int)raw[j + 1], xqr[s][j], dot, false);
+                    } else {
+                        ws = half_bits_to_float(raw[0]);
+#pragma unroll
+                        for (int j = 0; j < 8; ++j)
+                            dot = __builtin_amdgcn_sdot4((int)__builtin_amdgcn_alignbyte(raw[j + 1], raw[j], 2),
+                                                         xqr[s][j], dot, false);
+                    }
+                    // matvec.rs:148: `dot as f32 * (w_scale * x_scale)`
+                    prod[s] = (float)dot * (ws * xsr[s]);
+                }
+            }
+            // The block products in order, one after another.
+            float sum = -0.0f;
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                const int n_here = min(64, nb - 64 * s);
+                for (int l = 0; l < n_here; ++l) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(prod[s]), l));
+            }
+            acc[m] = sum;
+        }
+        if (lane == 0) {
+            float v = acc[0];
+            if constexpr (EPI == kSoftcap) v = tanhf(v * (1.0f / arg)) * arg;  // ops.rs:79-81
+            if constexpr (EPI == kGeglu) v = gelu_tanh(acc[0]) * acc[NM - 1];
+            if constexpr (EPI == kGegluFp16) v = gelu_tanh_fp16_table(acc[0]) * acc[NM - 1];
+            out[row] = v;
+        }
+    }
+}
+
+// Reads the 34-byte Q8_0 block at byte `off` of a row (2-byte aligned):
+// its f16 scale and the 32 values packed 4 to a dword.
+__device__ inline float load_q8_block(const unsigned short *row16, int64_t off, unsigned (&q)[8]) {
+    const unsigned short *p = row16 + off / 2;
+    const float scale = half_bits_to_float(p[0]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) q[j] = (unsigned)p[1 + 2 * j] | ((unsigned)p[2 + 2 * j] << 16);
+    return scale;
+}
+
+// Q8_0 against a Q8_0 activation, one lane per row (any cols multiple of 32):
+// the same block products and order as matvec_q8_0_kernel.
+template <int EPI>
+__global__ __launch_bounds__(256) void matvec_q8_0_rowwise_kernel(const unsigned char *__restrict__ w,
+                                                                  const unsigned char *__restrict__ w2,
+                                                                  int64_t rows, int nb, const float *__restrict__ xs,
+                                                                  const int *__restrict__ xq, float arg,
+                                                                  float *__restrict__ out) {
+#pragma clang fp contract(off)
+    const int64_t row = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (row >= rows) return;
+    constexpr int NM = EPI >= kGeglu ? 2 : 1;
+    const int64_t row_len = (int64_t)nb * kQ8Bytes;
+    float acc[NM];
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+        const unsigned short *r16 = (const unsigned short *)((m == 0 ? w : w2) + row * row_len);
+        float sum = -0.0f;
+        for (int b = 0; b < nb; ++b) {
+            unsigned q[8];
+            const float ws = load_q8_block(r16, (int64_t)b * kQ8Bytes, q);
+            int dot = 0;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) dot = __builtin_amdgcn_sdot4((int)q[j], xq[b * 8 + j], dot, false);
+            sum += (float)dot * (ws * xs[b]);
+        }
+        acc[m] = sum;
+    }
+    float v = acc[0];
+    if constexpr (EPI == kSoftcap) v = tanhf(v * (1.0f / arg)) * arg;
+    if constexpr (EPI == kGeglu) v = gelu_tanh(acc[0]) * acc[NM - 1];
+    if constexpr (EPI == kGegluFp16) v = gelu_tanh_fp16_table(acc[0]) * acc[NM - 1];
+    out[row] = v;
+}
+
+// matvec_q8_0_f32 / matvec_q8_0_f64_sums (matvec.rs:104-122, 153-176): f32
+// activations against dequantized blocks, one lane per row.  Per block the
+// 32 products summed in order, times the scale; the blocks summed in order
+// (F64: every sum in f64, one rounding at the end).
+template <bool F64>
+__global__ __launch_bounds__(256) void matvec_q8_0_f32_kernel(const unsigned char *__restrict__ w, int64_t rows,
+                                                              int nb, const float *__restrict__ x,
+                                                              float *__restrict__ out) {
+#pragma clang fp contract(off)
+    const int64_t row = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (row >= rows) return;
+    const unsigned short *r16 = (const unsigned short *)(w + row * (int64_t)nb * kQ8Bytes);
+    using T = typename std::conditional<F64, double, float>::type;
+    T sum = (T)-0.0;
+    for (int b = 0; b < nb; ++b) {
+        unsigned q[8];
+        const float scale = load_q8_block(r16, (int64_t)b * kQ8Bytes, q);
+        T dot = (T)-0.0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int v = (int)(signed char)(q[j] >> (8 * k));
+                dot += (T)v * (T)x[b * kQ8Values + 4 * j + k];
+            }
+        sum += dot * (T)scale;
+    }
+    out[row] = (float)sum;
+}
+
+// matvec.rs:196-204 (f32_to_bf16) and 192-194.
+__device__ inline float round_to_bf16(float value) {
+    const unsigned bits = __float_as_uint(value);
+    unsigned h;
+    if (value != value)
+        h = (bits >> 16) | 64u;
+    else
+        h = (bits + (0x7fffu + ((bits >> 16) & 1u))) >> 16;
+    return __uint_as_float(h << 16);
+}
+
+// matvec_bf16 (matvec.rs:124-130, 178-180): x rounded to bf16, one lane per
+// row, one sequential f32 sum over the row.
+__global__ __launch_bounds__(256) void matvec_bf16_kernel(const unsigned short *__restrict__ w, int64_t rows,
+                                                          int64_t cols, const float *__restrict__ x,
+                                                          float *__restrict__ out) {
+#pragma clang fp contract(off)
+    const int64_t row = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (row >= rows) return;
+    const unsigned short *r = w + row * cols;
+    float sum = -0.0f;
+    for (int64_t i = 0; i < cols; ++i) sum += __uint_as_float((unsigned)r[i] << 16) * round_to_bf16(x[i]);
+    out[row] = sum;
+}
+
+// matvec_f32 (matvec.rs:132-136, 182-184): one lane per row, sequential sum.
+__global__ __launch_bounds__(256) void matvec_f32_kernel(const float *__restrict__ w, int64_t rows, int64_t cols,
+                                                         const float *__restrict__ x, float *__restrict__ out) {
+#pragma clang fp contract(off)
+    const int64_t row = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (row >= rows) return;
+    const float *r = w + row * cols;
+    float sum = -0.0f;
+    for (int64_t i = 0; i < cols; ++i) sum += r[i] * x[i];
+    out[row] = sum;
+}
+
+template <int EPI, int NS>
+int launch_q8_rows(const MatvecArgs &a, int rpw, hipStream_t stream) {
+    constexpr int NM = EPI >= kGeglu ? 2 : 1;
+    const int nb = (int)(a.cols / kQ8Values);
+    const size_t lds = (size_t)4 * rpw * NM * (nb * kQ8Bytes);
+    const int64_t groups = (a.rows + 4 * rpw - 1) / (4 * rpw);
+    hipLaunchKernelGGL((matvec_q8_0_kernel<EPI, NS>), dim3((unsigned)groups), dim3(256), lds, stream, a.w, a.w2,
+                       a.rows, nb, a.xs, (const int *)a.xq, a.arg, rpw, a.out);
+    G4_HIP(hipGetLastError());
+    return G4_OK;
+}
+
+template <int EPI>
+int launch_q8(const MatvecArgs &a, int num_cus, hipStream_t stream) {
+    constexpr int NM = EPI >= kGeglu ? 2 : 1;
+    const int64_t nb = a.cols / kQ8Values;
+    // Rows start 16-byte aligned when cols is a multiple of 256 and the
+    // matrices are (GGUF aligns tensor data to 32 bytes).
+    const bool aligned = ((uintptr_t)a.w % 16 == 0) && (NM == 1 || (uintptr_t)a.w2 % 16 == 0);
+    if (a.cols % 256 == 0 && nb <= 256 && aligned) {
+        // Rows per wavefront: at most 16 KB of LDS per wave, and enough
+        // workgroups for two per CU.
+        const int64_t row_bytes = nb * kQ8Bytes * NM;
+        int64_t rpw = std::min<int64_t>(4, std::max<int64_t>(1, 16384 / row_bytes));
+        rpw = std::max<int64_t>(1, std::min<int64_t>(rpw, a.rows / (4LL * 2 * num_cus)));
+        const int ns = (int)((nb + 63) / 64);
+        switch (ns) {
+        case 1: return launch_q8_rows<EPI, 1>(a, (int)rpw, stream);
+        case 2: return launch_q8_rows<EPI, 2>(a, (int)rpw, stream);
+        case 3: return launch_q8_rows<EPI, 3>(a, (int)rpw, stream);
+        default: return launch_q8_rows<EPI, 4>(a, (int)rpw, stream);
+        }
+    }
+    hipLaunchKernelGGL((matvec_q8_0_rowwise_kernel<EPI>), dim3((unsigned)((a.rows + 255) / 256)), dim3(256), 0,
+                       stream, a.w, a.w2, a.rows, (int)nb, a.xs, (const int *)a.xq, a.arg, a.out);
+    G4_HIP(hipGetLastError());
+    return G4_OK;
+}
+
+}  // namespace
+
+int launch_quantize_q8_0(const float *x, int64_t n, float *scales, signed char *quants, hipStream_t stream) {
+    if (n <= 0) return G4_OK;
+    hipLaunchKernelGGL(quantize_q8_0_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, x, n, scales,
+                       quants);
+    G4_HIP(hipGetLastError());
+    return G4_OK;
+}
+
+int launch_matvec(g4_ctx *ctx, const MatvecArgs &a, hipStream_t stream) {
+    if (a.rows <= 0) return G4_OK;
+    const unsigned grid = (unsigned)((a.rows + 255) / 256);
+    switch (a.kind) {
+    case MatvecKind::Q8: return launch_q8<kPlain>(a, ctx->num_cus, stream);
+    case MatvecKind::Q8Softcap: return launch_q8<kSoftcap>(a, ctx->num_cus, stream);
+    case MatvecKind::Q8Geglu: return launch_q8<kGeglu>(a, ctx->num_cus, stream);
+    case MatvecKind::Q8GegluFp16: return launch_q8<kGegluFp16>(a, ctx->num_cus, stream);
+    case MatvecKind::Q8F32:
+        hipLaunchKernelGGL(matvec_q8_0_f32_kernel<false>, dim3(grid), dim3(256), 0, stream, a.w, a.rows,
+                           (int)(a.cols / kQ8Values), a.x, a.out);
+        break;
+    case MatvecKind::Q8F64:
+        hipLaunchKernelGGL(matvec_q8_0_f32_kernel<true>, dim3(grid), dim3(256), 0, stream, a.w, a.rows,
+                           (int)(a.cols / kQ8Values), a.x, a.out);
+        break;
+    case MatvecKind::Bf16:
+        hipLaunchKernelGGL(matvec_bf16_kernel, dim3(grid), dim3(256), 0, stream, (const unsigned short *)a.w, a.rows,
+                           a.cols, a.x, a.out);
+        break;
+    case MatvecKind::F32:
+        hipLaunchKernelGGL(matvec_f32_kernel, dim3(grid), dim3(256), 0, stream, (const float *)a.w, a.rows, a.cols,
+                           a.x, a.out);
+        break;
+    }
+    G4_HIP(hipGetLastError());
+    return G4_OK;
+}
+
+}  // namespace g4

@@ -77,6 +77,13 @@ _SIGS = {
                                c_vp, c_vp, c_vp, c_i64, c_vp]),
     "g4_layer_prefill": (c_int, [c_vp, c_vp, c_vp, c_int, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                                  ctypes.POINTER(c_int), c_vp]),
+    "g4_quantize_q8_0": (c_int, [c_vp, c_vp, c_i64, c_vp, c_vp, c_vp]),
+    "g4_matvec_q8_0": (c_int, [c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp]),
+    "g4_matvec_q8_0_softcap": (c_int, [c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_f32, c_vp, c_vp]),
+    "g4_geglu_q8_0": (c_int, [c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_int, c_vp, c_vp]),
+    "g4_matvec_q8_0_f32": (c_int, [c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_int, c_vp, c_vp]),
+    "g4_matvec_bf16": (c_int, [c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp]),
+    "g4_matvec_f32": (c_int, [c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp]),
     "g4_layer_is_global": (c_int, [c_int, c_int]),
     "g4_kv_source_layer": (c_int, [c_int, c_int, c_int, ctypes.POINTER(c_int)]),
     "g4_windowed_len": (None, [c_i64, c_i64, ctypes.POINTER(c_i64), ctypes.POINTER(c_i64)]),
@@ -249,6 +256,32 @@ class Context:
         _raise(lib().g4_prepare_qkv(self.handle, _ptr(q), _ptr(k), _ptr(v), n_tokens, pos0, n_heads, n_kv_heads,
                                     head_dim, _ptr(q_norm_w), _ptr(k_norm_w), eps, rope_base, _ptr(freq_factors),
                                     _ptr(k_rows), _ptr(v_rows), row_stride, _stream(stream)))
+
+    # -- mat-vecs over GGUF weight formats -----------------------------------
+    def quantize_q8_0(self, x, n, scales, quants, stream=None):
+        _raise(lib().g4_quantize_q8_0(self.handle, _ptr(x), n, _ptr(scales), _ptr(quants), _stream(stream)))
+
+    def matvec_q8_0(self, w, rows, cols, xs, xq, out, softcap=None, stream=None):
+        if softcap is None:
+            _raise(lib().g4_matvec_q8_0(self.handle, _ptr(w), w.numel(), rows, cols, _ptr(xs), _ptr(xq), _ptr(out),
+                                        _stream(stream)))
+        else:
+            _raise(lib().g4_matvec_q8_0_softcap(self.handle, _ptr(w), w.numel(), rows, cols, _ptr(xs), _ptr(xq),
+                                                softcap, _ptr(out), _stream(stream)))
+
+    def geglu_q8_0(self, gate, up, rows, cols, xs, xq, out, fp16_gelu=False, stream=None):
+        _raise(lib().g4_geglu_q8_0(self.handle, _ptr(gate), _ptr(up), gate.numel(), rows, cols, _ptr(xs), _ptr(xq),
+                                   int(fp16_gelu), _ptr(out), _stream(stream)))
+
+    def matvec_q8_0_f32(self, w, rows, cols, x, out, f64_sums=False, stream=None):
+        _raise(lib().g4_matvec_q8_0_f32(self.handle, _ptr(w), w.numel(), rows, cols, _ptr(x), int(f64_sums),
+                                        _ptr(out), _stream(stream)))
+
+    def matvec_bf16(self, w, rows, cols, x, out, stream=None):
+        _raise(lib().g4_matvec_bf16(self.handle, _ptr(w), w.numel(), rows, cols, _ptr(x), _ptr(out), _stream(stream)))
+
+    def matvec_f32(self, w, rows, cols, x, out, stream=None):
+        _raise(lib().g4_matvec_f32(self.handle, _ptr(w), w.numel(), rows, cols, _ptr(x), _ptr(out), _stream(stream)))
 
     # -- ComputePort -------------------------------------------------------
     def port_matmul(self, a, b, m, n, k, out, stream=None):

@@ -212,6 +212,45 @@ void g4_windowed_len(int64_t seq_len, int64_t window, int64_t *begin, int64_t *e
 /* proportional_rope_freq_factors (idea/mod.rs:162-165), out[head_dim/2] host. */
 void g4_proportional_rope_freq_factors(int head_dim, float p, float *out_host);
 
+/* -------------- mat-vecs over GGUF weight formats (crates/llm-backend-cpu/src/matvec.rs) */
+/* Weights are row-major [rows][cols] in their GGUF storage: Q8_0 rows of
+ * cols/32 blocks of 34 bytes (f16 scale, 32 int8), BF16 or f32 values.
+ * Results are bit-identical to the reference's (same per-block integer dots,
+ * same f32 products, sums in the reference's order); only tanh in GELU and
+ * the soft-cap comes from the device libm.  Shape errors carry the
+ * reference's messages ("Q8_0 weight has N elements, expected R rows of L"). */
+
+/* quantize_q8_0 (matvec.rs:35-53): x_dev [n], n a multiple of 32 ->
+ * scales_dev [n/32] (each the f16 rounding of max|x|/127, as f32) and
+ * quants_dev [n]. */
+int g4_quantize_q8_0(g4_ctx *ctx, const float *x_dev, int64_t n, float *scales_dev,
+                     int8_t *quants_dev, g4_stream stream);
+/* matvec_q8_0 (matvec.rs:55-62): out_dev[rows] = W @ x for a Q8_0 activation
+ * (x_scales_dev [cols/32], x_quants_dev [cols]); w_bytes = rows*cols/32*34. */
+int g4_matvec_q8_0(g4_ctx *ctx, const uint8_t *w_dev, int64_t w_bytes, int64_t rows, int64_t cols,
+                   const float *x_scales_dev, const int8_t *x_quants_dev, float *out_dev,
+                   g4_stream stream);
+/* matvec_q8_0_then(.., softcap, cap) (matvec.rs:64-81, model.rs:447):
+ * cap * tanh(logit / cap) on every output -- the final logits. */
+int g4_matvec_q8_0_softcap(g4_ctx *ctx, const uint8_t *w_dev, int64_t w_bytes, int64_t rows,
+                           int64_t cols, const float *x_scales_dev, const int8_t *x_quants_dev,
+                           float cap, float *out_dev, g4_stream stream);
+/* geglu_q8_0 (matvec.rs:83-102): gelu(gate_row . x) * (up_row . x); gelu is
+ * gelu_tanh, or gelu_tanh_fp16_table when fp16_gelu (ops.rs:85-103). */
+int g4_geglu_q8_0(g4_ctx *ctx, const uint8_t *gate_dev, const uint8_t *up_dev, int64_t w_bytes,
+                  int64_t rows, int64_t cols, const float *x_scales_dev,
+                  const int8_t *x_quants_dev, int fp16_gelu, float *out_dev, g4_stream stream);
+/* matvec_q8_0_f32 / matvec_q8_0_f64_sums (matvec.rs:104-122): an f32
+ * activation against dequantized blocks; f64_sums takes every sum in f64. */
+int g4_matvec_q8_0_f32(g4_ctx *ctx, const uint8_t *w_dev, int64_t w_bytes, int64_t rows, int64_t cols,
+                       const float *x_dev, int f64_sums, float *out_dev, g4_stream stream);
+/* matvec_bf16 (matvec.rs:124-130): x rounded to bf16 first, as ggml does. */
+int g4_matvec_bf16(g4_ctx *ctx, const uint16_t *w_dev, int64_t w_len, int64_t rows, int64_t cols,
+                   const float *x_dev, float *out_dev, g4_stream stream);
+/* matvec_f32 (matvec.rs:132-136). */
+int g4_matvec_f32(g4_ctx *ctx, const float *w_dev, int64_t w_len, int64_t rows, int64_t cols,
+                  const float *x_dev, float *out_dev, g4_stream stream);
+
 /* ------------------------------------- ComputePort (crates/llm-eng/src/compute.rs:3-29) */
 /* HipPort: the trait's method set on device buffers, with CpuPort's
  * semantics (crates/llm-backend-cpu/src/port.rs:11-51). */

@@ -29,6 +29,8 @@ static int fail(int code, const char *msg) {
 
 const char *or_last_error(void) { return last_error; }
 
+int or_fail(int code, const char *msg) { return fail(code, msg); }
+
 /* Rust's `Iterator::sum` for floats folds from -0.0 (neutral element of +). */
 #define SUM_START (-0.0f)
 

@@ -112,6 +112,34 @@ int or_layer_attention(or_kv_cache *c, const or_hparams *hp, size_t layer, size_
                        const float *k_norm_w, const float *rope_freqs, size_t n_freqs,
                        float *out, size_t *source_layer, size_t *kv_begin, size_t *kv_end);
 
+/* Records `msg` as the last error and returns `code`. */
+int or_fail(int code, const char *msg);
+
+/* ---- mat-vecs over GGUF weight formats (crates/llm-backend-cpu/src/matvec.rs) ---- */
+#define OR_Q8_BLOCK 32 /* values per Q8_0 block */
+#define OR_Q8_BYTES 34 /* f16 scale + 32 int8 */
+float or_f16_to_f32(uint16_t h);
+uint16_t or_f32_to_f16(float f);                                                 /* half::f16::from_f32 */
+float or_bf16_to_f32(uint16_t b);                                                /* matvec.rs:192-194 */
+uint16_t or_f32_to_bf16(float f);                                                /* matvec.rs:196-204 */
+int or_quantize_q8_0(const float *x, size_t n, float *scales, int8_t *quants);  /* matvec.rs:35-53 */
+int or_dequant_q8_0(const uint8_t *bytes, size_t len, float *out);              /* dequant.rs:13-24 */
+int or_matvec_q8_0(const uint8_t *w, size_t w_len, size_t rows, size_t cols, const float *xs,
+                   const int8_t *xq, float *out);                                /* matvec.rs:55-62 */
+int or_matvec_q8_0_softcap(const uint8_t *w, size_t w_len, size_t rows, size_t cols,
+                           const float *xs, const int8_t *xq, float cap, float *out); /* :64-81 */
+int or_geglu_q8_0(const uint8_t *gate, const uint8_t *up, size_t w_len, size_t rows, size_t cols,
+                  const float *xs, const int8_t *xq, int fp16_gelu, float *out); /* :83-102 */
+int or_matvec_q8_0_f32(const uint8_t *w, size_t w_len, size_t rows, size_t cols, const float *x,
+                       int f64_sums, float *out);                                /* :104-122 */
+int or_matvec_bf16(const uint16_t *w, size_t w_len, size_t rows, size_t cols, const float *x,
+                   float *out);                                                  /* :124-130 */
+int or_matvec_f32(const float *w, size_t w_len, size_t rows, size_t cols, const float *x,
+                  float *out);                                                   /* :132-136 */
+float or_softcap(float value, float cap);                                        /* ops.rs:79-81 */
+float or_gelu_tanh(float x);                                                     /* ops.rs:85-89 */
+float or_gelu_tanh_fp16_table(float x);                                          /* ops.rs:95-103 */
+
 /* ---- test and CPU-baseline helpers (not part of the reference) ---- */
 size_t or_pool_threads(void);
 /* Test inputs: for each of n_rows rows of row_width floats, norm_heads with

@@ -83,6 +83,21 @@ def lib():
                                                   c_vp, c_vp, c_vp, c_size, c_vp, ctypes.POINTER(c_size),
                                                   ctypes.POINTER(c_size), ctypes.POINTER(c_size)]),
             "or_pool_threads": (c_size, []),
+            "or_f16_to_f32": (c_f32, [ctypes.c_uint16]),
+            "or_f32_to_f16": (ctypes.c_uint16, [c_f32]),
+            "or_bf16_to_f32": (c_f32, [ctypes.c_uint16]),
+            "or_f32_to_bf16": (ctypes.c_uint16, [c_f32]),
+            "or_quantize_q8_0": (ctypes.c_int, [c_vp, c_size, c_vp, c_vp]),
+            "or_dequant_q8_0": (ctypes.c_int, [c_vp, c_size, c_vp]),
+            "or_matvec_q8_0": (ctypes.c_int, [c_vp, c_size, c_size, c_size, c_vp, c_vp, c_vp]),
+            "or_matvec_q8_0_softcap": (ctypes.c_int, [c_vp, c_size, c_size, c_size, c_vp, c_vp, c_f32, c_vp]),
+            "or_geglu_q8_0": (ctypes.c_int, [c_vp, c_vp, c_size, c_size, c_size, c_vp, c_vp, ctypes.c_int, c_vp]),
+            "or_matvec_q8_0_f32": (ctypes.c_int, [c_vp, c_size, c_size, c_size, c_vp, ctypes.c_int, c_vp]),
+            "or_matvec_bf16": (ctypes.c_int, [c_vp, c_size, c_size, c_size, c_vp, c_vp]),
+            "or_matvec_f32": (ctypes.c_int, [c_vp, c_size, c_size, c_size, c_vp, c_vp]),
+            "or_softcap": (c_f32, [c_f32, c_f32]),
+            "or_gelu_tanh": (c_f32, [c_f32]),
+            "or_gelu_tanh_fp16_table": (c_f32, [c_f32]),
             "or_prepare_rows": (ctypes.c_int, [c_vp, c_size, c_size, c_size, c_vp, c_f32, c_size, c_f32, c_vp,
                                                c_size]),
         }
@@ -284,3 +299,95 @@ def prepare_rows(x, head_dim, weight=None, eps=1e-6, pos0=0, base=0.0, freq_fact
                                  None if w is None else w.ctypes.data, eps, pos0, base,
                                  None if f is None else f.ctypes.data, 0 if f is None else f.size))
     return x
+
+
+# ---------------------------------------------- mat-vecs over GGUF weight formats
+def _u8(a):
+    return np.ascontiguousarray(a, dtype=np.uint8)
+
+
+def f16_to_f32(h):
+    return lib().or_f16_to_f32(int(h))
+
+
+def f32_to_f16(x):
+    return lib().or_f32_to_f16(float(x))
+
+
+def bf16_to_f32(b):
+    return lib().or_bf16_to_f32(int(b))
+
+
+def f32_to_bf16(x):
+    return lib().or_f32_to_bf16(float(x))
+
+
+def quantize_q8_0(x):
+    """quantize_q8_0 (matvec.rs:35-53): (scales f32 [n/32], quants int8 [n])."""
+    x = _f32(x)
+    scales = np.zeros(max(x.size // 32, 1), np.float32)
+    quants = np.zeros(max(x.size, 1), np.int8)
+    _check(lib().or_quantize_q8_0(x.ctypes.data, x.size, scales.ctypes.data, quants.ctypes.data))
+    return scales[: x.size // 32], quants[: x.size]
+
+
+def dequant_q8_0(data):
+    data = _u8(data)
+    out = np.zeros(max(data.size // 34 * 32, 1), np.float32)
+    _check(lib().or_dequant_q8_0(data.ctypes.data, data.size, out.ctypes.data))
+    return out[: data.size // 34 * 32]
+
+
+def matvec_q8_0(w, rows, cols, xs, xq, softcap=None):
+    w, xs, xq = _u8(w), _f32(xs), np.ascontiguousarray(xq, np.int8)
+    out = np.zeros(max(rows, 1), np.float32)
+    if softcap is None:
+        _check(lib().or_matvec_q8_0(w.ctypes.data, w.size, rows, cols, xs.ctypes.data, xq.ctypes.data,
+                                    out.ctypes.data))
+    else:
+        _check(lib().or_matvec_q8_0_softcap(w.ctypes.data, w.size, rows, cols, xs.ctypes.data, xq.ctypes.data,
+                                            softcap, out.ctypes.data))
+    return out[:rows]
+
+
+def geglu_q8_0(gate, up, rows, cols, xs, xq, fp16_gelu=False):
+    gate, up, xs, xq = _u8(gate), _u8(up), _f32(xs), np.ascontiguousarray(xq, np.int8)
+    assert gate.size == up.size
+    out = np.zeros(max(rows, 1), np.float32)
+    _check(lib().or_geglu_q8_0(gate.ctypes.data, up.ctypes.data, gate.size, rows, cols, xs.ctypes.data,
+                               xq.ctypes.data, int(fp16_gelu), out.ctypes.data))
+    return out[:rows]
+
+
+def matvec_q8_0_f32(w, rows, cols, x, f64_sums=False):
+    w, x = _u8(w), _f32(x)
+    out = np.zeros(max(rows, 1), np.float32)
+    _check(lib().or_matvec_q8_0_f32(w.ctypes.data, w.size, rows, cols, x.ctypes.data, int(f64_sums),
+                                    out.ctypes.data))
+    return out[:rows]
+
+
+def matvec_bf16(w, rows, cols, x):
+    w, x = np.ascontiguousarray(w, np.uint16), _f32(x)
+    out = np.zeros(max(rows, 1), np.float32)
+    _check(lib().or_matvec_bf16(w.ctypes.data, w.size, rows, cols, x.ctypes.data, out.ctypes.data))
+    return out[:rows]
+
+
+def matvec_f32(w, rows, cols, x):
+    w, x = _f32(w), _f32(x)
+    out = np.zeros(max(rows, 1), np.float32)
+    _check(lib().or_matvec_f32(w.ctypes.data, w.size, rows, cols, x.ctypes.data, out.ctypes.data))
+    return out[:rows]
+
+
+def softcap(v, cap):
+    return lib().or_softcap(float(v), float(cap))
+
+
+def gelu_tanh(x):
+    return lib().or_gelu_tanh(float(x))
+
+
+def gelu_tanh_fp16_table(x):
+    return lib().or_gelu_tanh_fp16_table(float(x))

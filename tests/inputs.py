@@ -73,3 +73,31 @@ def rel_err(a, b):
     b = np.asarray(b, np.float64)
     scale = np.maximum(np.maximum(np.abs(a), np.abs(b)), 1.0)
     return float(np.max(np.abs(a - b) / scale)) if a.size else 0.0
+
+
+# ------------------------------------------------- mat-vec inputs (Q8_0, BF16)
+def lcg_values(seed, n):
+    """The reference mat-vec tests' input generator
+    (crates/llm-backend-cpu/tests/matvec.rs:9-18): a 64-bit LCG, values in [-1, 1)."""
+    out = np.empty(n, np.float32)
+    state = seed
+    for i in range(n):
+        state = (state * 6364136223846793005 + 1) % (1 << 64)
+        out[i] = np.float32(state >> 40) / np.float32(1 << 23) - np.float32(1.0)
+    return out
+
+
+def q8_0_bytes(weights):
+    """Q8_0 bytes of a row-major matrix as the reference tests build them
+    (tests/matvec.rs:21-31): per 32 values an f16 scale max|w|/127, then the
+    values w/scale rounded half away from zero (NaN -> 0), saturated."""
+    blocks = np.asarray(weights, np.float32).reshape(-1, 32)
+    scale = np.abs(blocks).max(axis=1) / np.float32(127.0)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        q = blocks / scale[:, None]
+    r = np.where(np.isnan(q), 0.0, np.sign(q) * np.floor(np.abs(q) + 0.5))
+    qi = np.clip(r, -128, 127).astype(np.int8)
+    out = np.empty((blocks.shape[0], 34), np.uint8)
+    out[:, :2] = scale.astype(np.float16).view(np.uint8).reshape(-1, 2)
+    out[:, 2:] = qi.view(np.uint8)
+    return out.reshape(-1)

@@ -319,7 +319,8 @@ def test_planted_mistakes_are_caught(plant, tmp_path):
     root = os.path.dirname(HERE)
     so = tmp_path / "liboracle.so"
     subprocess.run(["gcc", "-O1", "-std=c11", "-fPIC", "-shared", "-ffp-contract=off", f"-D{plant}",
-                    "-o", str(so), os.path.join(root, "oracle", "g4_oracle.c"), "-lm", "-lpthread"], check=True)
+                    "-o", str(so), os.path.join(root, "oracle", "g4_oracle.c"),
+                    os.path.join(root, "oracle", "g4_oracle_matvec.c"), "-lm", "-lpthread"], check=True)
     env = dict(os.environ, G4_ORACLE_LIB=str(so))
     r = subprocess.run([sys.executable, "-m", "pytest", "-q", "-x", "-p", "no:cacheprovider",
                         f"{__file__}::{PLANTS[plant]}"], env=env, cwd=root, capture_output=True, text=True)
