@@ -16,7 +16,8 @@ restatement of the reference's CPU attention, same `concat` copy and per-head
 thread pool) timed on this host's cores on a bounded sample of the same step.
 `workloads` carries the other measured shapes (sliding decode, the 35-layer
 stack, 2048-token prefill, the ragged 32-sequence batch, the layer drivers with
-their fused input preparation).
+their fused input preparation, the Q8_0 mat-vecs of the output head and a
+projection).
 """
 import argparse
 import json
@@ -246,6 +247,37 @@ def bench_layer_steps(ctx, torch, prep, steps, warmup, T=4096, N=2048):
     return res
 
 
+def bench_matvec(ctx, torch, steps, warmup, rows=262144, cols=1536, cap=30.0):
+    """The output head of E2B as the reference benchmarks it
+    (crates/llm-backend-cpu/examples/bench_matvec.rs): a 262,144 x 1536 Q8_0
+    matrix (428 MB, larger than the Infinity Cache) against the quantized
+    final hidden state, with the logit soft-cap fused; plus the E2B global
+    layer's q projection (4096 x 1536)."""
+    res = {}
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(77)
+    for name, r, c, softcap in (("logits_262144x1536_softcap", rows, cols, cap), ("q_proj_4096x1536", 4096, cols, None)):
+        nb = c // 32
+        w = torch.randint(-127, 128, (r, nb, 34), dtype=torch.int32, device="cuda", generator=gen).to(torch.uint8)
+        w[:, :, 0:2] = torch.tensor([0x1F, 0x21], dtype=torch.uint8, device="cuda")  # f16 scale ~0.01
+        w = w.reshape(-1)
+        x = torch.randn(c, device="cuda", generator=gen)
+        xs = torch.empty(c // 32, device="cuda")
+        xq = torch.empty(c, dtype=torch.int8, device="cuda")
+        out = torch.empty(r, device="cuda")
+
+        def step(i):
+            ctx.quantize_q8_0(x, c, xs, xq)
+            ctx.matvec_q8_0(w, r, c, xs, xq, out, softcap=softcap)
+
+        wall, ev = time_steps(torch, step, steps, warmup, block=10)
+        nbytes = r * nb * 34 + c * 4 + r * 4
+        res[name] = {"us": ev / steps * 1e6, "gbs": nbytes / (ev / steps) / 1e9, "bytes": nbytes,
+                     "frac_of_hbm_peak": nbytes / (ev / steps) / 1e9 / HBM_PEAK_GBS}
+        del w
+    return res
+
+
 def bench_ragged(ctx, torch, prep, steps, warmup, B=32, seed=2024):
     import numpy as np
     lens = np.random.default_rng(seed).integers(1024, 32768 + 1, size=B).astype(np.int64)
@@ -333,7 +365,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-workloads", action="store_true", help="only the headline step")
-    ap.add_argument("--only", choices=["global", "sliding", "stack", "prefill", "ragged", "layer", "copy"],
+    ap.add_argument("--only", choices=["global", "sliding", "stack", "prefill", "ragged", "layer", "matvec", "copy"],
                     help="run one workload alone (for profiling); prints its result.  'copy' is a "
                          "plain 256 MiB device copy, the reference point for HBM byte counters")
     args = ap.parse_args()
@@ -356,6 +388,7 @@ def main():
                   "prefill": lambda: bench_prefill(ctx, torch, prep, max(5, k // 10), 2),
                   "ragged": lambda: bench_ragged(ctx, torch, prep, max(5, k // 4), 2),
                   "layer": lambda: bench_layer_steps(ctx, torch, prep, args.steps, args.warmup),
+                  "matvec": lambda: bench_matvec(ctx, torch, max(20, k // 2), 5),
                   "copy": lambda: bench_copy(torch, max(5, k // 4))}[args.only]
             res = fn()
             res.pop("host", None)
@@ -374,6 +407,7 @@ def main():
             workloads["prefill_2048"] = bench_prefill(ctx, torch, prep, max(5, k // 10), 2)
             workloads["ragged_decode_B32"] = bench_ragged(ctx, torch, prep, max(5, k // 4), 2)
             workloads["layer_drivers"] = bench_layer_steps(ctx, torch, prep, args.steps, args.warmup)
+            workloads["q8_0_matvec"] = bench_matvec(ctx, torch, max(20, k // 2), 5)
         workloads["global_decode_d512_ctx4096_warm"] = {
             "us_per_layer": g["event_warm"] / args.steps * 1e6,
             "gbs": g["bytes"] / (g["event_warm"] / args.steps) / 1e9,

@@ -10,12 +10,13 @@
 // comes from the device's libm.
 //
 // Q8_0 with quantized activations (the engine's default numerics) is the
-// HBM-bound hot path: a wavefront takes whole rows, streams each row's bytes
-// into LDS with 16-byte loads (rows of 34-byte blocks are 16-byte aligned
-// when cols is a multiple of 256), and lane b then takes block b: its f16
-// scale and 32 int8 values against the activation's block b (held in the
-// lane's registers for the whole kernel), 8 v_dot4 steps.  The block
-// products are then summed in order by reading them lane by lane.  The
+// HBM-bound hot path: a wavefront takes a run of rows, streams their bytes
+// into LDS with 16-byte direct-to-LDS loads (rows of 34-byte blocks are
+// 16-byte aligned when cols is a multiple of 256), and lane b then takes
+// block b: its f16 scale and 32 int8 values against the activation's block b
+// (held in the lane's registers for the whole kernel), 8 v_dot4 steps.  The
+// block products go to a table in LDS that lane r then sums for row r in
+// block order, so the run's sequential sums proceed side by side.  The
 // other formats, which the engine uses only for small tensors or for its
 // comparison numerics, give each lane one row and sum sequentially.
 
@@ -89,23 +90,31 @@ __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *x, int6
 // Epilogues of the Q8_0 row kernel.
 enum Epilogue : int { kPlain = 0, kSoftcap = 1, kGeglu = 2, kGegluFp16 = 3 };
 
-// W @ x for Q8_0 rows against a Q8_0 activation (matvec.rs:55-102).
-// NS = activation blocks per lane (blocks b = lane + 64 s).  Each wavefront
-// handles `rpw` consecutive rows, all loaded into its LDS area before any is
-// used; kGeglu* read a second matrix (up) beside the first (gate).
+// W @ x for Q8_0 rows against a Q8_0 activation (matvec.rs:55-102).  A
+// workgroup is one wavefront and takes `rb` consecutive rows (rb <= 64), staged into
+// LDS `g` rows at a time with direct-to-LDS 16-byte loads.  For each staged
+// row, lane b computes block b's product (NS = blocks per lane: b = lane +
+// 64 s) into a row-major product table in LDS; once all rows are done, lane
+// r sums row r's products in block order -- up to 64 independent sequential
+// sums at once, each exactly the reference's.  kGeglu* read a second matrix
+// (up) beside the first (gate).  Large matrices stage one row at a time in
+// small workgroups, so that many are resident per CU (measured faster than
+// double-buffering fewer of them); small ones stage all their rows at once.
 template <int EPI, int NS>
-__global__ __launch_bounds__(256) void matvec_q8_0_kernel(const unsigned char *__restrict__ w,
-                                                          const unsigned char *__restrict__ w2, int64_t rows,
-                                                          int nb, const float *__restrict__ xs,
-                                                          const int *__restrict__ xq, float arg, int rpw,
-                                                          float *__restrict__ out) {
+__global__ __launch_bounds__(64) void matvec_q8_0_kernel(const unsigned char *__restrict__ w,
+                                                         const unsigned char *__restrict__ w2, int64_t rows,
+                                                         int nb, const float *__restrict__ xs,
+                                                         const int *__restrict__ xq, float arg, int g, int rb,
+                                                         float *__restrict__ out) {
 #pragma clang fp contract(off)
-    extern __shared__ u32x4 stage[];
+    extern __shared__ u32x4 lds[];
     constexpr int NM = EPI >= kGeglu ? 2 : 1;  // matrices read
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x;
     const int row_len = nb * kQ8Bytes;  // bytes, a multiple of 16
     const int chunks = row_len >> 4;    // 16-byte chunks per row
-    u32x4 *my = stage + (size_t)wave * rpw * NM * chunks;
+    const int pstride = nb + 1;         // product table row stride (odd: no bank conflicts)
+    u32x4 *stage = lds;                                  // [g][NM][chunks]
+    float *prod = (float *)(lds + (size_t)g * NM * chunks);  // [NM][rb][pstride]
 
     // This lane's activation blocks: 8 packed int8 dwords and the scale.
     int xqr[NS][8];
@@ -118,79 +127,74 @@ __global__ __launch_bounds__(256) void matvec_q8_0_kernel(const unsigned char *_
         xsr[s] = b < nb ? xs[b] : 0.0f;
     }
 
-    const int64_t row0 = ((int64_t)blockIdx.x * 4 + wave) * rpw;
-    // Stage rpw rows (of each matrix) in LDS with direct-to-LDS loads, all
-    // issued before any is waited for; rows past the end are not read.
-    for (int m = 0; m < NM; ++m) {
-        const unsigned char *src = m == 0 ? w : w2;
-        for (int r = 0; r < rpw; ++r) {
-            const int64_t row = row0 + r;
-            if (row >= rows) break;
-            const __amdgpu_buffer_rsrc_t rs =
-                __builtin_amdgcn_make_buffer_rsrc((void *)(src + row * row_len), 0, row_len, kBufferWord3);
-            u32x4 *dst = my + (r * NM + m) * chunks;
-            for (int k = 0; k * 64 < chunks; ++k)
-                if (k * 64 + lane < chunks) load_to_lds(rs, dst + 64 * k, (uint32_t)(k * 64 + lane) * 16u);
-        }
-    }
-    __builtin_amdgcn_s_waitcnt(kVmcntZero);
-    __syncthreads();
-
-    for (int r = 0; r < rpw; ++r) {
-        const int64_t row = row0 + r;
-        if (row >= rows) break;
-        float acc[NM];
+    const int64_t row0 = (int64_t)blockIdx.x * rb;
+    const int n_rows = (int)min((int64_t)rb, rows - row0);
+    for (int r0 = 0; r0 < n_rows; r0 += g) {
+        const int nr = min(g, n_rows - r0);
+        // Stage rows r0 .. r0 + nr - 1 of each matrix.
+        for (int r = 0; r < nr; ++r)
 #pragma unroll
-        for (int m = 0; m < NM; ++m) {
-            const unsigned *rw = (const unsigned *)(my + (r * NM + m) * chunks);
-            float prod[NS];
+            for (int m = 0; m < NM; ++m) {
+                const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                    (void *)((m == 0 ? w : w2) + (row0 + r0 + r) * row_len), 0, row_len, kBufferWord3);
+                u32x4 *dst = stage + (r * NM + m) * chunks;
+                for (int k = 0; k * 64 < chunks; ++k)
+                    if (k * 64 + lane < chunks) load_to_lds(rs, dst + 64 * k, (uint32_t)(k * 64 + lane) * 16u);
+            }
+        __builtin_amdgcn_s_waitcnt(kVmcntZero);
+        __syncthreads();
+        for (int r = 0; r < nr; ++r)
 #pragma unroll
-            for (int s = 0; s < NS; ++s) {
-                const int b = lane + 64 * s;
-                prod[s] = 0.0f;
-                if (b < nb) {
-                    // Block b starts at byte 34b: dword 17(b/2), offset 0
-                    // (even b: scale in the low half, values from byte 2)
-                    // or dword 17(b/2) + 8, offset 2 (odd b: scale in the
-                    // high half, values dword-aligned after it).
-                    const unsigned *d = rw + 17 * (b >> 1) + ((b & 1) ? 8 : 0);
-                    unsigned raw[9];
+            for (int m = 0; m < NM; ++m) {
+                const unsigned *rw = (const unsigned *)(stage + (r * NM + m) * chunks);
+                float *pr = prod + ((size_t)m * rb + r0 + r) * pstride;
 #pragma unroll
-                    for (int j = 0; j < 9; ++j) raw[j] = d[j];
-                    int dot = 0;
-                    float ws;
-                    if (b & 1) {
-                        ws = half_bits_to_float(raw[0] >> 16);
+                for (int s = 0; s < NS; ++s) {
+                    const int b = lane + 64 * s;
+                    if (b < nb) {
+                        // Block b starts at byte 34b: dword 17(b/2), offset 0
+                        // (even b: scale in the low half, values from byte 2)
+                        // or dword 17(b/2) + 8, offset 2 (odd b: scale in the
+                        // high half, values dword-aligned after it).
+                        const unsigned *d = rw + 17 * (b >> 1) + ((b & 1) ? 8 : 0);
+                        unsigned raw[9];
 #pragma unroll
-                        for (int j = 0; j < 8; ++j) dot = __builtin_amdgcn_sdot4((int)raw[j + 1], xqr[s][j], dot, false);
-                    } else {
-                        ws = half_bits_to_float(raw[0]);
+                        for (int j = 0; j < 9; ++j) raw[j] = d[j];
+                        int dot = 0;
+                        float ws;
+                        if (b & 1) {
+                            ws = half_bits_to_float(raw[0] >> 16);
 #pragma unroll
-                        for (int j = 0; j < 8; ++j)
-                            dot = __builtin_amdgcn_sdot4((int)__builtin_amdgcn_alignbyte(raw[j + 1], raw[j], 2),
-                                                         xqr[s][j], dot, false);
+                            for (int j = 0; j < 8; ++j) dot = __builtin_amdgcn_sdot4((int)raw[j + 1], xqr[s][j], dot, false);
+                        } else {
+                            ws = half_bits_to_float(raw[0]);
+#pragma unroll
+                            for (int j = 0; j < 8; ++j)
+                                dot = __builtin_amdgcn_sdot4((int)__builtin_amdgcn_alignbyte(raw[j + 1], raw[j], 2),
+                                                             xqr[s][j], dot, false);
+                        }
+                        // matvec.rs:148: `dot as f32 * (w_scale * x_scale)`
+                        pr[b] = (float)dot * (ws * xsr[s]);
                     }
-                    // matvec.rs:148: `dot as f32 * (w_scale * x_scale)`
-                    prod[s] = (float)dot * (ws * xsr[s]);
                 }
             }
-            // The block products in order, one after another.
-            float sum = -0.0f;
-#pragma unroll
-            for (int s = 0; s < NS; ++s) {
-                const int n_here = min(64, nb - 64 * s);
-                for (int l = 0; l < n_here; ++l) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(prod[s]), l));
-            }
-            acc[m] = sum;
-        }
-        if (lane == 0) {
-            float v = acc[0];
-            if constexpr (EPI == kSoftcap) v = tanhf(v * (1.0f / arg)) * arg;  // ops.rs:79-81
-            if constexpr (EPI == kGeglu) v = gelu_tanh(acc[0]) * acc[NM - 1];
-            if constexpr (EPI == kGegluFp16) v = gelu_tanh_fp16_table(acc[0]) * acc[NM - 1];
-            out[row] = v;
-        }
+        __syncthreads();  // the stage is refilled next; the products are complete
     }
+    if (lane >= n_rows) return;
+    // Lane r: row r's block products summed in block order.
+    float acc[NM];
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+        const float *pr = prod + ((size_t)m * rb + lane) * pstride;
+        float sum = -0.0f;
+        for (int b = 0; b < nb; ++b) sum += pr[b];
+        acc[m] = sum;
+    }
+    float v = acc[0];
+    if constexpr (EPI == kSoftcap) v = tanhf(v * (1.0f / arg)) * arg;  // ops.rs:79-81
+    if constexpr (EPI == kGeglu) v = gelu_tanh(acc[0]) * acc[NM - 1];
+    if constexpr (EPI == kGegluFp16) v = gelu_tanh_fp16_table(acc[0]) * acc[NM - 1];
+    out[row0 + lane] = v;
 }
 
 // Reads the 34-byte Q8_0 block at byte `off` of a row (2-byte aligned):
@@ -306,13 +310,13 @@ __global__ __launch_bounds__(256) void matvec_f32_kernel(const float *__restrict
 }
 
 template <int EPI, int NS>
-int launch_q8_rows(const MatvecArgs &a, int rpw, hipStream_t stream) {
+int launch_q8_rows(const MatvecArgs &a, int g, int rb, hipStream_t stream) {
     constexpr int NM = EPI >= kGeglu ? 2 : 1;
     const int nb = (int)(a.cols / kQ8Values);
-    const size_t lds = (size_t)4 * rpw * NM * (nb * kQ8Bytes);
-    const int64_t groups = (a.rows + 4 * rpw - 1) / (4 * rpw);
-    hipLaunchKernelGGL((matvec_q8_0_kernel<EPI, NS>), dim3((unsigned)groups), dim3(256), lds, stream, a.w, a.w2,
-                       a.rows, nb, a.xs, (const int *)a.xq, a.arg, rpw, a.out);
+    const size_t lds = (size_t)g * NM * (nb * kQ8Bytes) + (size_t)NM * rb * (nb + 1) * sizeof(float);
+    const int64_t groups = (a.rows + rb - 1) / rb;
+    hipLaunchKernelGGL((matvec_q8_0_kernel<EPI, NS>), dim3((unsigned)groups), dim3(64), lds, stream, a.w, a.w2,
+                       a.rows, nb, a.xs, (const int *)a.xq, a.arg, g, rb, a.out);
     G4_HIP(hipGetLastError());
     return G4_OK;
 }
@@ -325,17 +329,27 @@ int launch_q8(const MatvecArgs &a, int num_cus, hipStream_t stream) {
     // matrices are (GGUF aligns tensor data to 32 bytes).
     const bool aligned = ((uintptr_t)a.w % 16 == 0) && (NM == 1 || (uintptr_t)a.w2 % 16 == 0);
     if (a.cols % 256 == 0 && nb <= 256 && aligned) {
-        // Rows per wavefront: at most 16 KB of LDS per wave, and enough
-        // workgroups for two per CU.
-        const int64_t row_bytes = nb * kQ8Bytes * NM;
-        int64_t rpw = std::min<int64_t>(4, std::max<int64_t>(1, 16384 / row_bytes));
-        rpw = std::max<int64_t>(1, std::min<int64_t>(rpw, a.rows / (4LL * 2 * num_cus)));
+        // Large matrices: 16 rows per workgroup, staged one at a time, so
+        // that the workgroups are small and many are resident per CU
+        // (measured faster than staging or double-buffering more rows in
+        // fewer of them).  Small ones: a workgroup's rows all in flight at
+        // once, and about eight workgroups per CU.  The product table stays
+        // under 16 KB.
+        const int64_t rb_max = std::min<int64_t>(16, std::max<int64_t>(1, 16384 / (NM * (nb + 1) * 4)));
+        int64_t rb, g;
+        if (a.rows >= rb_max * 8 * num_cus) {
+            rb = rb_max;
+            g = 1;
+        } else {
+            rb = std::max<int64_t>(1, std::min<int64_t>(rb_max, a.rows / (8LL * num_cus)));
+            g = rb;
+        }
         const int ns = (int)((nb + 63) / 64);
         switch (ns) {
-        case 1: return launch_q8_rows<EPI, 1>(a, (int)rpw, stream);
-        case 2: return launch_q8_rows<EPI, 2>(a, (int)rpw, stream);
-        case 3: return launch_q8_rows<EPI, 3>(a, (int)rpw, stream);
-        default: return launch_q8_rows<EPI, 4>(a, (int)rpw, stream);
+        case 1: return launch_q8_rows<EPI, 1>(a, (int)g, (int)rb, stream);
+        case 2: return launch_q8_rows<EPI, 2>(a, (int)g, (int)rb, stream);
+        case 3: return launch_q8_rows<EPI, 3>(a, (int)g, (int)rb, stream);
+        default: return launch_q8_rows<EPI, 4>(a, (int)g, (int)rb, stream);
         }
     }
     hipLaunchKernelGGL((matvec_q8_0_rowwise_kernel<EPI>), dim3((unsigned)((a.rows + 255) / 256)), dim3(256), 0,
