@@ -262,13 +262,13 @@ def bench_matvec(ctx, torch, steps, warmup, rows=262144, cols=1536, cap=30.0):
         w[:, :, 0:2] = torch.tensor([0x1F, 0x21], dtype=torch.uint8, device="cuda")  # f16 scale ~0.01
         w = w.reshape(-1)
         x = torch.randn(c, device="cuda", generator=gen)
-        xs = torch.empty(c // 32, device="cuda")
-        xq = torch.empty(c, dtype=torch.int8, device="cuda")
         out = torch.empty(r, device="cuda")
 
-        def step(i):
-            ctx.quantize_q8_0(x, c, xs, xq)
-            ctx.matvec_q8_0(w, r, c, xs, xq, out, softcap=softcap)
+        def step(i):  # quantize_q8_0 + mat-vec (+ soft-cap), one launch
+            if softcap is None:
+                ctx.project_q8_0(w, r, c, x, out)
+            else:
+                ctx.logits_q8_0(w, r, c, x, softcap, out)
 
         wall, ev = time_steps(torch, step, steps, warmup, block=10)
         nbytes = r * nb * 34 + c * 4 + r * 4

@@ -691,9 +691,11 @@ int q8_cols_error(const char *what, int64_t cols) {
                                              " is not a multiple of 32");
 }
 
-// The Q8_0-activation forms: matvec, softcap, geglu.
+// The Q8_0-activation forms: matvec, softcap, geglu; with x (and no xs/xq)
+// the activation is quantized as part of the call.
 int q8_matvec(g4_ctx *ctx, g4::MatvecKind kind, const uint8_t *w, const uint8_t *w2, int64_t w_bytes, int64_t rows,
-              int64_t cols, const float *xs, const int8_t *xq, float arg, float *out, g4_stream stream) {
+              int64_t cols, const float *xs, const int8_t *xq, float arg, float *out, g4_stream stream,
+              const float *x = nullptr) {
     if (!ctx) return invalid("mat-vec: null context");
     if (cols < 0 || cols % 32 != 0) return q8_cols_error("activation length", cols);
     const int rc = check_weight_shape("Q8_0", w_bytes, rows, cols / 32 * 34);
@@ -706,12 +708,40 @@ int q8_matvec(g4_ctx *ctx, g4::MatvecKind kind, const uint8_t *w, const uint8_t 
     a.cols = cols;
     a.xs = xs;
     a.xq = (const signed char *)xq;
+    a.x = x;
     a.arg = arg;
     a.out = out;
     return g4::launch_matvec(ctx, a, as_stream(stream));
 }
 
 }  // namespace
+
+int g4_project_q8_0(g4_ctx *ctx, const uint8_t *w, int64_t w_bytes, int64_t rows, int64_t cols, const float *x,
+                    float *out, g4_stream stream) {
+    return guarded([&] {
+        g4::clear_error();
+        return q8_matvec(ctx, g4::MatvecKind::Q8, w, nullptr, w_bytes, rows, cols, nullptr, nullptr, 0.0f, out,
+                         stream, x);
+    });
+}
+
+int g4_gated_ffn_q8_0(g4_ctx *ctx, const uint8_t *gate, const uint8_t *up, int64_t w_bytes, int64_t rows,
+                      int64_t cols, const float *x, int fp16_gelu, float *out, g4_stream stream) {
+    return guarded([&] {
+        g4::clear_error();
+        return q8_matvec(ctx, fp16_gelu ? g4::MatvecKind::Q8GegluFp16 : g4::MatvecKind::Q8Geglu, gate, up, w_bytes,
+                         rows, cols, nullptr, nullptr, 0.0f, out, stream, x);
+    });
+}
+
+int g4_logits_q8_0(g4_ctx *ctx, const uint8_t *w, int64_t w_bytes, int64_t rows, int64_t cols, const float *x,
+                   float cap, float *out, g4_stream stream) {
+    return guarded([&] {
+        g4::clear_error();
+        return q8_matvec(ctx, g4::MatvecKind::Q8Softcap, w, nullptr, w_bytes, rows, cols, nullptr, nullptr, cap,
+                         out, stream, x);
+    });
+}
 
 int g4_quantize_q8_0(g4_ctx *ctx, const float *x, int64_t n, float *scales, int8_t *quants, g4_stream stream) {
     return guarded([&] {

@@ -126,7 +126,8 @@ struct MatvecArgs {
     int64_t rows, cols;
     const float *xs;          // Q8_0 activation: block scales [cols/32]
     const signed char *xq;    // Q8_0 activation: values [cols]
-    const float *x;           // f32 activation [cols] (Q8F32, Q8F64, Bf16, F32)
+    const float *x;           // f32 activation [cols] (Q8F32, Q8F64, Bf16, F32; the Q8 kinds
+                              // quantize it themselves when xs is null)
     float arg;                // soft-cap
     float *out;               // [rows]
 };

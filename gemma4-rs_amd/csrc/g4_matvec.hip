@@ -87,6 +87,31 @@ __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *x, int6
     quants[i] = (signed char)saturate_i8(rintf(v * inverse));
 }
 
+// One lane's quantize_q8_0 of block b of x (16-byte aligned): the same
+// arithmetic as quantize_q8_0_kernel, the 32 values packed 4 to a dword.
+__device__ inline float quantize_block(const float *x, int b, int (&q)[8]) {
+#pragma clang fp contract(off)
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    f32x4 v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = ((const f32x4 *)(x + kQ8Values * b))[j];
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) m = fmaxf(m, fabsf(v[j][k]));
+    const float scale = m / 127.0f;
+    const float inverse = scale == 0.0f ? 0.0f : 1.0f / scale;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        unsigned packed = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) packed |= ((unsigned)saturate_i8(rintf(v[j][k] * inverse)) & 0xffu) << (8 * k);
+        q[j] = (int)packed;
+    }
+    return round_to_half(scale);
+}
+
 // Epilogues of the Q8_0 row kernel.
 enum Epilogue : int { kPlain = 0, kSoftcap = 1, kGeglu = 2, kGegluFp16 = 3 };
 
@@ -104,8 +129,8 @@ template <int EPI, int NS>
 __global__ __launch_bounds__(64) void matvec_q8_0_kernel(const unsigned char *__restrict__ w,
                                                          const unsigned char *__restrict__ w2, int64_t rows,
                                                          int nb, const float *__restrict__ xs,
-                                                         const int *__restrict__ xq, float arg, int g, int rb,
-                                                         float *__restrict__ out) {
+                                                         const int *__restrict__ xq, const float *__restrict__ xf,
+                                                         float arg, int g, int rb, float *__restrict__ out) {
 #pragma clang fp contract(off)
     extern __shared__ u32x4 lds[];
     constexpr int NM = EPI >= kGeglu ? 2 : 1;  // matrices read
@@ -123,8 +148,17 @@ __global__ __launch_bounds__(64) void matvec_q8_0_kernel(const unsigned char *__
     for (int s = 0; s < NS; ++s) {
         const int b = lane + 64 * s;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) xqr[s][j] = b < nb ? xq[b * 8 + j] : 0;
-        xsr[s] = b < nb ? xs[b] : 0.0f;
+        for (int j = 0; j < 8; ++j) xqr[s][j] = 0;
+        xsr[s] = 0.0f;
+        if (b < nb) {
+            if (xf) {  // quantize_q8_0 of the f32 activation, here
+                xsr[s] = quantize_block(xf, b, xqr[s]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) xqr[s][j] = xq[b * 8 + j];
+                xsr[s] = xs[b];
+            }
+        }
     }
 
     const int64_t row0 = (int64_t)blockIdx.x * rb;
@@ -316,28 +350,44 @@ int launch_q8_rows(const MatvecArgs &a, int g, int rb, hipStream_t stream) {
     const size_t lds = (size_t)g * NM * (nb * kQ8Bytes) + (size_t)NM * rb * (nb + 1) * sizeof(float);
     const int64_t groups = (a.rows + rb - 1) / rb;
     hipLaunchKernelGGL((matvec_q8_0_kernel<EPI, NS>), dim3((unsigned)groups), dim3(64), lds, stream, a.w, a.w2,
-                       a.rows, nb, a.xs, (const int *)a.xq, a.arg, g, rb, a.out);
+                       a.rows, nb, a.xs, (const int *)a.xq, a.xs ? nullptr : a.x, a.arg, g, rb, a.out);
     G4_HIP(hipGetLastError());
     return G4_OK;
 }
 
 template <int EPI>
-int launch_q8(const MatvecArgs &a, int num_cus, hipStream_t stream) {
+int launch_q8(g4_ctx *ctx, MatvecArgs a, hipStream_t stream) {
     constexpr int NM = EPI >= kGeglu ? 2 : 1;
+    const int num_cus = ctx->num_cus;
     const int64_t nb = a.cols / kQ8Values;
     // Rows start 16-byte aligned when cols is a multiple of 256 and the
     // matrices are (GGUF aligns tensor data to 32 bytes).
-    const bool aligned = ((uintptr_t)a.w % 16 == 0) && (NM == 1 || (uintptr_t)a.w2 % 16 == 0);
-    if (a.cols % 256 == 0 && nb <= 256 && aligned) {
-        // Large matrices: 16 rows per workgroup, staged one at a time, so
-        // that the workgroups are small and many are resident per CU
+    const bool aligned = ((uintptr_t)a.w % 16 == 0) && (NM == 1 || (uintptr_t)a.w2 % 16 == 0) &&
+                         (a.xs || (uintptr_t)a.x % 16 == 0);
+    const bool fast = a.cols % 256 == 0 && nb <= 256 && aligned;
+    // Rows per workgroup: up to 16, the product table under 16 KB.
+    const int64_t rb_max = std::min<int64_t>(16, std::max<int64_t>(1, 16384 / (NM * (nb + 1) * 4)));
+    const bool large = a.rows >= rb_max * 8 * num_cus;
+    if (!a.xs && (!fast || large)) {
+        // An f32 activation for a kernel that reads a quantized one, or a
+        // matrix large enough that its many workgroups would each quantize
+        // it again: quantize_q8_0 into the context's workspace first.
+        const size_t sbytes = ((size_t)nb * sizeof(float) + 255) / 256 * 256;
+        const int rc = ensure_workspace(ctx, sbytes + (size_t)a.cols, stream);
+        if (rc != G4_OK) return rc;
+        a.xs = (const float *)ctx->ws.ptr;
+        a.xq = (const signed char *)ctx->ws.ptr + sbytes;
+        const int rq = launch_quantize_q8_0(a.x, a.cols, (float *)a.xs, (signed char *)a.xq, stream);
+        if (rq != G4_OK) return rq;
+    }
+    if (fast) {
+        // Large matrices: rb_max rows per workgroup, staged one at a time,
+        // so that the workgroups are small and many are resident per CU
         // (measured faster than staging or double-buffering more rows in
         // fewer of them).  Small ones: a workgroup's rows all in flight at
-        // once, and about eight workgroups per CU.  The product table stays
-        // under 16 KB.
-        const int64_t rb_max = std::min<int64_t>(16, std::max<int64_t>(1, 16384 / (NM * (nb + 1) * 4)));
+        // once, and about eight workgroups per CU.
         int64_t rb, g;
-        if (a.rows >= rb_max * 8 * num_cus) {
+        if (large) {
             rb = rb_max;
             g = 1;
         } else {
@@ -372,10 +422,10 @@ int launch_matvec(g4_ctx *ctx, const MatvecArgs &a, hipStream_t stream) {
     if (a.rows <= 0) return G4_OK;
     const unsigned grid = (unsigned)((a.rows + 255) / 256);
     switch (a.kind) {
-    case MatvecKind::Q8: return launch_q8<kPlain>(a, ctx->num_cus, stream);
-    case MatvecKind::Q8Softcap: return launch_q8<kSoftcap>(a, ctx->num_cus, stream);
-    case MatvecKind::Q8Geglu: return launch_q8<kGeglu>(a, ctx->num_cus, stream);
-    case MatvecKind::Q8GegluFp16: return launch_q8<kGegluFp16>(a, ctx->num_cus, stream);
+    case MatvecKind::Q8: return launch_q8<kPlain>(ctx, a, stream);
+    case MatvecKind::Q8Softcap: return launch_q8<kSoftcap>(ctx, a, stream);
+    case MatvecKind::Q8Geglu: return launch_q8<kGeglu>(ctx, a, stream);
+    case MatvecKind::Q8GegluFp16: return launch_q8<kGegluFp16>(ctx, a, stream);
     case MatvecKind::Q8F32:
         hipLaunchKernelGGL(matvec_q8_0_f32_kernel<false>, dim3(grid), dim3(256), 0, stream, a.w, a.rows,
                            (int)(a.cols / kQ8Values), a.x, a.out);

@@ -82,6 +82,9 @@ _SIGS = {
     "g4_matvec_q8_0_softcap": (c_int, [c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_f32, c_vp, c_vp]),
     "g4_geglu_q8_0": (c_int, [c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_int, c_vp, c_vp]),
     "g4_matvec_q8_0_f32": (c_int, [c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_int, c_vp, c_vp]),
+    "g4_project_q8_0": (c_int, [c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp]),
+    "g4_gated_ffn_q8_0": (c_int, [c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_int, c_vp, c_vp]),
+    "g4_logits_q8_0": (c_int, [c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_f32, c_vp, c_vp]),
     "g4_matvec_bf16": (c_int, [c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp]),
     "g4_matvec_f32": (c_int, [c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp]),
     "g4_layer_is_global": (c_int, [c_int, c_int]),
@@ -272,6 +275,17 @@ class Context:
     def geglu_q8_0(self, gate, up, rows, cols, xs, xq, out, fp16_gelu=False, stream=None):
         _raise(lib().g4_geglu_q8_0(self.handle, _ptr(gate), _ptr(up), gate.numel(), rows, cols, _ptr(xs), _ptr(xq),
                                    int(fp16_gelu), _ptr(out), _stream(stream)))
+
+    def project_q8_0(self, w, rows, cols, x, out, stream=None):
+        _raise(lib().g4_project_q8_0(self.handle, _ptr(w), w.numel(), rows, cols, _ptr(x), _ptr(out), _stream(stream)))
+
+    def gated_ffn_q8_0(self, gate, up, rows, cols, x, out, fp16_gelu=False, stream=None):
+        _raise(lib().g4_gated_ffn_q8_0(self.handle, _ptr(gate), _ptr(up), gate.numel(), rows, cols, _ptr(x),
+                                       int(fp16_gelu), _ptr(out), _stream(stream)))
+
+    def logits_q8_0(self, w, rows, cols, x, cap, out, stream=None):
+        _raise(lib().g4_logits_q8_0(self.handle, _ptr(w), w.numel(), rows, cols, _ptr(x), cap, _ptr(out),
+                                    _stream(stream)))
 
     def matvec_q8_0_f32(self, w, rows, cols, x, out, f64_sums=False, stream=None):
         _raise(lib().g4_matvec_q8_0_f32(self.handle, _ptr(w), w.numel(), rows, cols, _ptr(x), int(f64_sums),

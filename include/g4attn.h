@@ -240,6 +240,18 @@ int g4_matvec_q8_0_softcap(g4_ctx *ctx, const uint8_t *w_dev, int64_t w_bytes, i
 int g4_geglu_q8_0(g4_ctx *ctx, const uint8_t *gate_dev, const uint8_t *up_dev, int64_t w_bytes,
                   int64_t rows, int64_t cols, const float *x_scales_dev,
                   const int8_t *x_quants_dev, int fp16_gelu, float *out_dev, g4_stream stream);
+/* The model-level calls with the activation quantization folded in (one
+ * launch; the same results as g4_quantize_q8_0 followed by the call above):
+ * `project` with quantized activations (model.rs:211-212), the GELU-gated
+ * FFN input (model.rs:236-237) and the soft-capped logits (model.rs:447).
+ * x_dev [cols] f32. */
+int g4_project_q8_0(g4_ctx *ctx, const uint8_t *w_dev, int64_t w_bytes, int64_t rows, int64_t cols,
+                    const float *x_dev, float *out_dev, g4_stream stream);
+int g4_gated_ffn_q8_0(g4_ctx *ctx, const uint8_t *gate_dev, const uint8_t *up_dev, int64_t w_bytes,
+                      int64_t rows, int64_t cols, const float *x_dev, int fp16_gelu, float *out_dev,
+                      g4_stream stream);
+int g4_logits_q8_0(g4_ctx *ctx, const uint8_t *w_dev, int64_t w_bytes, int64_t rows, int64_t cols,
+                   const float *x_dev, float cap, float *out_dev, g4_stream stream);
 /* matvec_q8_0_f32 / matvec_q8_0_f64_sums (matvec.rs:104-122): an f32
  * activation against dequantized blocks; f64_sums takes every sum in f64. */
 int g4_matvec_q8_0_f32(g4_ctx *ctx, const uint8_t *w_dev, int64_t w_bytes, int64_t rows, int64_t cols,

@@ -169,3 +169,29 @@ def test_shape_errors(ctx):
         ctx.matvec_q8_0_f32(dev(np.zeros(34, np.uint8)), 1, 33, dev(np.ones(33, np.float32)), out)
     with pytest.raises(g4hip.EngError, match="BF16 weight has 3 elements, expected 1 rows of 2"):
         ctx.matvec_bf16(dev(np.zeros(3, np.uint16)), 1, 2, dev(np.ones(2, np.float32)), out)
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 256), (2048, 1536), (300, 96), (3, 8192)])
+def test_fused_quantization_entries_equal_the_two_step_calls(ctx, rows, cols):
+    """project / gated FFN / logits with the activation quantized inside the
+    call: bit for bit the quantize_q8_0 + mat-vec pair (model.rs:211-212,
+    236-237, 447).  An f32 activation that is not 16-byte aligned and column
+    counts outside the LDS-staged kernel take the two-step route inside."""
+    gate = dev(I.q8_0_bytes(matrix(8, rows, cols)))
+    up = dev(I.q8_0_bytes(matrix(9, rows, cols)))
+    xh = np.random.default_rng(rows).standard_normal(cols + 1).astype(np.float32)
+    for x in (dev(xh[:cols]), dev(xh)[1:]):  # aligned, then 4 bytes off
+        xs = torch.empty(cols // 32, device="cuda")
+        xq = torch.empty(cols, dtype=torch.int8, device="cuda")
+        ctx.quantize_q8_0(x, cols, xs, xq)
+        a, b = torch.empty(rows, device="cuda"), torch.empty(rows, device="cuda")
+        ctx.matvec_q8_0(gate, rows, cols, xs, xq, a)
+        ctx.project_q8_0(gate, rows, cols, x, b)
+        assert torch.equal(a, b)
+        ctx.matvec_q8_0(gate, rows, cols, xs, xq, a, softcap=30.0)
+        ctx.logits_q8_0(gate, rows, cols, x, 30.0, b)
+        assert torch.equal(a, b)
+        for f16 in (False, True):
+            ctx.geglu_q8_0(gate, up, rows, cols, xs, xq, a, fp16_gelu=f16)
+            ctx.gated_ffn_q8_0(gate, up, rows, cols, x, b, fp16_gelu=f16)
+            assert torch.equal(a, b)
