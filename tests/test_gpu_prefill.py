@@ -78,3 +78,18 @@ def test_prefill_never_reads_future_or_out_of_window_rows(ctx):
     for i in (0, 1, N // 2, N - 1):
         b, e = I.attended_range(pos0 + i, W)
         assert I.rel_err(got[i], orc.attend(q[pos0 + i], K[b:e], V[b:e], 8, 1)) <= TOL
+
+
+@pytest.mark.parametrize("d,window,pos0,N", [(512, 0, 6000, 64), (512, 0, 0, 700), (256, 512, 3000, 300),
+                                             (512, 0, 12000, 24)])
+def test_prefill_long_contexts_and_unit_lengths(ctx, d, window, pos0, N):
+    """Chunks deep into a long context and chunk lengths whose unit table
+    uses other unit lengths than the 2048-token prompt's (the lengths are
+    chosen per shape); sampled rows against the oracle."""
+    print(f"[case] prefill d={d} W={window} pos0={pos0} N={N}", flush=True)
+    q, K, V = case(900 + d + pos0, pos0 + N, d, d == 512)
+    got = prefill(ctx, q[pos0:], K, V, pos0, N, window, d)
+    rows = sorted({0, 1, N // 2, N - 2, N - 1} | set(np.random.default_rng(pos0).integers(0, N, 12).tolist()))
+    for i in rows:
+        b, e = I.attended_range(pos0 + i, window)
+        assert I.rel_err(got[i], orc.attend(q[pos0 + i], K[b:e], V[b:e], 8, 1)) <= TOL, i
