@@ -43,8 +43,8 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kDecodeBuffers = 4;  // K/V tiles held per wave: a pair computed, a pair in flight
 constexpr int kMaxSplits = 512;  // per (sequence, KV head); bounds the split workspace
-// Wavefronts per split workgroup for head dim D.
-constexpr int decode_waves(int D) { return D == 512 ? 8 : 8; }
+// Wavefronts per split workgroup (both head widths: two per SIMD).
+constexpr int kDecodeWaves = 8;
 // The online softmax keeps a reference maximum m and moves it only when a
 // score exceeds it by more than this (natural-log units; p <= 2^8 meanwhile,
 // safe in f32), so the accumulators are rescaled a few times per split, not
@@ -114,7 +114,7 @@ __device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 // tile of a V row).
 template <int D>
 struct DecodeShape {
-    static constexpr int NW = decode_waves(D);
+    static constexpr int NW = kDecodeWaves;
     static constexpr int DW = D / NW;   // 32 or 64
     static constexpr int KU = DW / 16;  // 2 or 4
     static constexpr int TW = DW / 16;  // 2 or 4
