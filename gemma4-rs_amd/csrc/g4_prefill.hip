@@ -122,16 +122,20 @@ __device__ inline void load_to_lds(__amdgpu_buffer_rsrc_t rsrc, f32x4 *lds, uint
 // Workgroup geometry for head width D: 4 row groups of 16 rows, each owned by
 // SPLIT wavefronts that divide the head dimension (DH = D / SPLIT dims each),
 // so that one wavefront's Q^T and O^T fit the register file.
+//
+// At D = 256 a wavefront holds Q^T and O^T for the whole head (SPLIT = 1):
+// no exchange of partial scores, 64 KB of LDS, and two workgroups per CU.
+// At D = 512 the head does not fit one wavefront's registers (SPLIT = 2).
 template <int D>
 struct PrefillShape {
-    static constexpr int SPLIT = 2;  // the merge grid's z extent is WAVES
+    static constexpr int SPLIT = D == 256 ? 1 : 2;  // the merge grid's z extent is WAVES
     static constexpr int DH = D / SPLIT;
     static constexpr int WAVES = kWaves * SPLIT;
     static constexpr int THREADS = 64 * WAVES;
 };
 
 template <int D>
-__global__ __launch_bounds__(PrefillShape<D>::THREADS, 1) void prefill_kernel(PrefillK p) {
+__global__ __launch_bounds__(PrefillShape<D>::THREADS, PrefillShape<D>::SPLIT == 1 ? 2 : 1) void prefill_kernel(PrefillK p) {
     using S = PrefillShape<D>;
     constexpr int DH = S::DH;
     constexpr int NU = DH / 32;  // 32-dim K chunks per wave
