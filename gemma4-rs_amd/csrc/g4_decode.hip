@@ -39,6 +39,8 @@ namespace {
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kDecodeBuffers = 4;  // K/V tiles held per wave: a pair computed, a pair in flight
@@ -215,6 +217,9 @@ __device__ inline void write_merged(const DecodeK &p, int s, int kvh, int e, flo
 // Buffer resource (V#) word 3 for raw 32-bit-element buffers on gfx9-class
 // GPUs, gfx950 included.
 constexpr int kBufferWord3 = 0x00020000;
+// Cache-policy operand of a buffer store: SC1, device scope -- the store is
+// written through the XCD's L2 to the point of coherence.
+constexpr int kDeviceScope = 16;
 
 // A wavefront's view of one (sequence, KV head) decode: lane (g, c) =
 // (lane/16, lane%16) of wave w, which owns head dims [base, base + DW).
@@ -399,15 +404,27 @@ struct DecodeAcc {
     }
 
     // This wave's share of a split partial (see partial_dim0); `slot` is the
-    // partial's index in units of G*D floats / G (m, l) pairs.
+    // partial's index in units of G*D floats / G (m, l) pairs.  The stores
+    // are written through to the point of coherence: the merge kernel reads
+    // them from other XCDs, and the split kernel then ends with no dirty L2
+    // lines of its own to write back (measured 0.6 us faster per decode at
+    // 256 splits).
     __device__ __forceinline__ void write_partial(const L &ln, float *part_o, float2 *part_ml, int64_t slot, int G,
                                                   bool col_valid) const {
         const float lt = rows_sum(l);
         if (!col_valid) return;
-        f32x4 *po = (f32x4 *)(part_o + slot * G * D);
+        const __amdgpu_buffer_rsrc_t ro =
+            __builtin_amdgcn_make_buffer_rsrc((void *)(part_o + slot * G * D), 0, G * D * 4, kBufferWord3);
 #pragma unroll
-        for (int i = 0; i < TW; ++i) po[((ln.wave * TW + i) * 4 + ln.g) * G + ln.c] = o[i];
-        if (ln.wave == 0 && ln.g == 0) part_ml[slot * G + ln.c] = float2{m, lt};
+        for (int i = 0; i < TW; ++i)
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o[i]), ro,
+                                                   (((ln.wave * TW + i) * 4 + ln.g) * G + ln.c) * 16, 0, kDeviceScope);
+        if (ln.wave == 0 && ln.g == 0) {
+            const __amdgpu_buffer_rsrc_t rm =
+                __builtin_amdgcn_make_buffer_rsrc((void *)(part_ml + slot * G), 0, G * 8, kBufferWord3);
+            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{m, lt}), rm, ln.c * 8, 0,
+                                                  kDeviceScope);
+        }
     }
 };
 
