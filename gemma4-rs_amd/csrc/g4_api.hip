@@ -260,6 +260,19 @@ int g4_attend_prefill(g4_ctx *ctx, const float *q, const float *k_cache, const f
     });
 }
 
+int g4_prefill_schedule(int64_t pos0, int64_t N, int64_t window, int head_dim, int n_kv_heads, int num_cus,
+                        int32_t *units, int64_t units_cap, int32_t *bin_start, int64_t bins_cap, int32_t *counts) {
+    return guarded([&] {
+        g4::clear_error();
+        if (N <= 0 || pos0 < 0 || window < 0) return invalid("prefill schedule needs N > 0, pos0, window >= 0");
+        if (head_dim != 256 && head_dim != 512) return invalid("prefill schedule: head_dim must be 256 or 512");
+        if (n_kv_heads < 1 || num_cus < 1) return invalid("prefill schedule: n_kv_heads and num_cus must be positive");
+        if (!units || !bin_start || !counts) return invalid("prefill schedule: null output array");
+        return g4::describe_prefill_schedule(pos0, N, window, head_dim, n_kv_heads, num_cus, units, units_cap,
+                                             bin_start, bins_cap, counts);
+    });
+}
+
 int g4_attend(g4_ctx *ctx, const float *q_host, size_t q_len, const float *keys_host,
               const float *values_host, size_t T, size_t n_heads, size_t n_kv_heads, float scale,
               float *out_host) {

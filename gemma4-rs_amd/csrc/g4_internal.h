@@ -90,6 +90,10 @@ struct PrefillArgs {
 };
 int launch_prefill(g4_ctx *ctx, const PrefillArgs &a, hipStream_t stream);
 void release_prefill_plan(g4_ctx *ctx);
+// The prefill kernel's work schedule for a shape (host only).
+int describe_prefill_schedule(int64_t pos0, int64_t N, int64_t window, int head_dim, int n_kv_heads, int num_cus,
+                              int32_t *units4, int64_t units_cap, int32_t *bin_start, int64_t bins_cap,
+                              int32_t *counts);
 
 int launch_rms_norm_rows(const float *x, int64_t n_rows, int64_t width, const float *w, float eps,
                          float *out, hipStream_t stream);

@@ -17,13 +17,17 @@
 // the B-operand layout P^T needs, so P stays in registers.
 //
 // Work balance: the causal triangle gives the last position blocks many more
-// tiles than the first, so a block's key range is cut into units of at most
-// kPrefillUnitTiles tiles; units are ordered heaviest first.  A block with
-// one unit writes its output directly; otherwise each unit leaves an (m, l, O)
-// partial and a merge kernel combines them in unit order.
+// tiles than the first, so a block's key range may be cut into units (at
+// most kPrefillMaxUnitsDev per block), and the host assigns every unit to a
+// workgroup (at most one per CU), which runs its units in turn; the
+// schedule builder below explains the choice.  A block with one unit writes
+// its output directly; otherwise each unit leaves an (m, l, O) partial and a
+// merge kernel combines them in key order.
 
 #include <algorithm>
+#include <array>
 #include <functional>
+#include <queue>
 #include <utility>
 #include <vector>
 
@@ -43,7 +47,13 @@ constexpr int kWaves = 4;
 constexpr int kPosPerWave = 2;                       // 16 rows = 2 positions x 8 heads
 constexpr int kPosPerBlock = kWaves * kPosPerWave;   // 8
 constexpr int kGroup = 8;                            // query heads per KV head
-constexpr float kRescaleSlack = 8.0f / 1.4426950408889634f;  // 8 in log2 units
+// Lazy-rescaling slack, 32 in log2 units: a weight p = e^(s - m) stays
+// below 2^32, so l and O (sums of p and p*v over the keys) stay below
+// 2^32 * keys * max|v| -- far from the f32 limit 2^128 -- and the final O/l
+// is the same ratio whatever reference max m it was accumulated against.
+// Normalised Gemma queries and keys give scores spread over tens of units,
+// which a slack of 8 log2 units made rescale on most tiles.
+constexpr float kRescaleSlack = 32.0f / 1.4426950408889634f;
 constexpr int kPrefillMaxUnitsDev = 8;  // partial units per block (merge weight table)
 // Buffer resource (V#) word 3 for raw 32-bit-element buffers on gfx9-class
 // GPUs, gfx950 included.
@@ -70,7 +80,8 @@ struct PrefillK {
     int n_heads;
     float scale;
     float *out;
-    const PrefillUnit *units;
+    const PrefillUnit *units;      // grouped by workgroup
+    const int *bin_start;          // workgroup x runs units [bin_start[x], bin_start[x + 1])
     const PrefillBlockInfo *blocks;
     float *part_o;    // [slot][kv head][wave][D/16 tiles][64 lanes] f32x4
     float2 *part_ml;  // [slot][kv head][64 rows]
@@ -134,8 +145,10 @@ struct PrefillShape {
     static constexpr int THREADS = 64 * WAVES;
 };
 
+// One unit: the rows of position block u.block against its key tiles
+// [u.t_lo, u.t_hi), leaving the block's output or the unit's partial.
 template <int D>
-__global__ __launch_bounds__(PrefillShape<D>::THREADS, PrefillShape<D>::SPLIT == 1 ? 2 : 1) void prefill_kernel(PrefillK p) {
+__device__ __forceinline__ void prefill_unit(const PrefillK &p, const PrefillUnit u) {
     using S = PrefillShape<D>;
     constexpr int DH = S::DH;
     constexpr int NU = DH / 32;  // 32-dim K chunks per wave
@@ -149,7 +162,6 @@ __global__ __launch_bounds__(PrefillShape<D>::THREADS, PrefillShape<D>::SPLIT ==
     const int rg = wave % kWaves, half = wave / kWaves;  // row group, dim half
     const int g = lane >> 4, c = lane & 15;
     const int kvh = blockIdx.y;
-    const PrefillUnit u = p.units[blockIdx.x];
 
     const int64_t P0 = p.pos0 + (int64_t)kPosPerBlock * u.block;
     const int64_t last_pos = p.pos0 + p.N - 1;
@@ -299,8 +311,8 @@ __global__ __launch_bounds__(PrefillShape<D>::THREADS, PrefillShape<D>::SPLIT ==
         for (int r = 0; r < 4; ++r) bad |= __builtin_amdgcn_classf(sv[r], 0x203);  // signalling/quiet NaN, +inf
         const float mt = rows_max(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])));
         // Lazy rescaling: a row keeps its reference max m until a score
-        // exceeds it by more than kRescaleSlack (p <= 2^8 meanwhile, safe in
-        // f32), so O is rescaled a few times per row rather than every tile.
+        // exceeds it by more than kRescaleSlack (p < 2^32 meanwhile, safe in
+        // f32), so O is rescaled about once per row rather than every tile.
         if (__any(mt > m + kRescaleSlack)) {
             const float m_new = fmaxf(m, mt);
             const float alpha = (m_new == -INFINITY) ? 1.0f : exp2_fast((m - m_new) * kLog2e);
@@ -372,7 +384,19 @@ __global__ __launch_bounds__(PrefillShape<D>::THREADS, PrefillShape<D>::SPLIT ==
     }
 }
 
-// Combines the units of one position block (and KV head) in unit order for
+// A workgroup runs its units in turn (the host's schedule).
+template <int D>
+__global__ __launch_bounds__(PrefillShape<D>::THREADS, PrefillShape<D>::SPLIT == 1 ? 2 : 1) void prefill_kernel(PrefillK p) {
+    const int first = p.bin_start[blockIdx.x], end = p.bin_start[blockIdx.x + 1];
+    for (int i = first; i < end; ++i) {
+        // The previous unit's waves are done with the tile buffers (its
+        // spare tile loads landed before its epilogue).
+        if (i > first) __syncthreads();
+        prefill_unit<D>(p, p.units[i]);
+    }
+}
+
+// Combines the units of one position block (and KV head) in key order for
 // the rows and dims of one producing wavefront (blockIdx.z), then writes
 // them row-major through LDS.  The per-unit loads of an element are
 // unrolled so that they are all in flight together.
@@ -444,10 +468,10 @@ constexpr int kPrefillMaxUnits = kPrefillMaxUnitsDev;  // per position block
 // A unit table in device memory, for one prefill shape.
 struct PrefillPlan {
     int64_t pos0 = -1, N = -1, window = -1;
-    int head_dim = 0;
-    int unit_tiles = 0;
-    int n_units = 0, n_blocks = 0, n_slots = 0;
+    int head_dim = 0, n_kv_heads = 0;
+    int n_units = 0, n_bins = 0, n_blocks = 0, n_slots = 0;
     PrefillUnit *units = nullptr;
+    int *bin_start = nullptr;
     PrefillBlockInfo *blocks = nullptr;
     uint64_t last_use = 0;
 };
@@ -464,8 +488,10 @@ struct PrefillPlans {
 
 void free_plan(PrefillPlan &pl) {
     if (pl.units) (void)hipFree(pl.units);
+    if (pl.bin_start) (void)hipFree(pl.bin_start);
     if (pl.blocks) (void)hipFree(pl.blocks);
     pl.units = nullptr;
+    pl.bin_start = nullptr;
     pl.blocks = nullptr;
 }
 
@@ -486,103 +512,266 @@ void release_prefill_plan(g4_ctx *ctx) {
     ctx->prefill_plan = nullptr;
 }
 
-// Unit length (in 16-key tiles) for a shape.  The hardware hands
-// workgroups to CUs in order as they free up, one per CU (LDS-bound), so a
-// unit table sorted heaviest first runs as a greedy list schedule.  Each
-// candidate length is scored by simulating that schedule: a unit costs its
-// tiles plus 1.5 (prologue and epilogue), and splitting any block adds 3 (the
-// merge kernel); the cheapest candidate wins (ties: the longer units).  On
-// a 2048-token causal prompt this picks 48-tile units and beat the fixed 32
-// by 8% (as the simulation predicted).
-static int choose_unit_tiles(const std::vector<std::pair<int, int>> &block_tiles, int num_cus) {
+// Work schedule of a prefill shape.  A unit is the tiles [t_lo, t_hi) of one
+// position block; each workgroup runs a list of units (a bin) one after the
+// other, and the grid is at most one workgroup per CU per KV head, so every
+// bin starts at once and the host's assignment is the schedule: no
+// workgroup waits for the hardware to hand it a CU, and the split of the
+// key ranges is chosen knowing where each piece runs.
+//
+// Cost model, in tiles (one 16-key tile of 64 query rows): a unit costs its
+// tiles plus kUnitCost (loading Q, filling the tile pipeline, writing O or
+// the partial); blocks split into several units add a merge kernel of
+// kMergeBase + kMergePerPartial per partial.  Measured on MI355X at
+// d = 512: 4.9 us per tile, 9.1 us per unit (the fit over a 2048-token
+// causal prompt's 480 units), merge 17 us for 384 partials.
+constexpr double kUnitCost = 1.9;
+constexpr double kMergePerPartial = 0.009;
+constexpr int kMinUnitTiles = 4;  // a split leaves no piece shorter (unless the block is)
+
+using Piece = std::array<int, 3>;  // block, t_lo, t_hi
+using Bins = std::vector<std::vector<Piece>>;
+
+static double merge_cost(int partials, int head_dim) {
+    if (partials == 0) return 0.0;
+    return (head_dim == 512 ? 0.6 : 1.2) + kMergePerPartial * partials;
+}
+
+// Makespan plus merge cost; nullopt-like -1 when a block has more pieces
+// than the merge kernel combines.
+static double schedule_cost(const Bins &bins, int n_blocks, int head_dim) {
+    std::vector<int> pieces(n_blocks, 0);
+    double makespan = 0.0;
+    for (auto &bin : bins) {
+        double load = 0.0;
+        for (auto &pc : bin) {
+            load += pc[2] - pc[1] + kUnitCost;
+            ++pieces[pc[0]];
+        }
+        makespan = std::max(makespan, load);
+    }
+    int partials = 0;
+    for (int n : pieces) {
+        if (n > kPrefillMaxUnits) return -1.0;
+        if (n > 1) partials += n;
+    }
+    return makespan + merge_cost(partials, head_dim);
+}
+
+// Fixed-length units (each block cut into ceil(tiles / ut) near-equal
+// pieces) assigned heaviest first to the least loaded bin.
+static Bins lpt_bins(const std::vector<std::pair<int, int>> &bt, int ut, int n_bins) {
+    std::vector<Piece> units;
+    for (int b = 0; b < (int)bt.size(); ++b) {
+        const int t_lo = bt[b].first, tiles = bt[b].second - t_lo, nu = (tiles + ut - 1) / ut;
+        for (int j = 0; j < nu; ++j) units.push_back({b, t_lo + j * tiles / nu, t_lo + (j + 1) * tiles / nu});
+    }
+    std::stable_sort(units.begin(), units.end(),
+                     [](const Piece &x, const Piece &y) { return x[2] - x[1] > y[2] - y[1]; });
+    Bins bins((size_t)n_bins);
+    using Load = std::pair<double, int>;
+    std::priority_queue<Load, std::vector<Load>, std::greater<Load>> heap;
+    for (int i = 0; i < n_bins; ++i) heap.push({0.0, i});
+    for (auto &u : units) {
+        Load l = heap.top();
+        heap.pop();
+        bins[l.second].push_back(u);
+        heap.push({l.first + (u[2] - u[1]) + kUnitCost, l.second});
+    }
+    return bins;
+}
+
+// Stream-K packing at capacity `cap`: blocks in the order largest,
+// smallest, second largest, second smallest, ... fill the bins in turn; a
+// block that does not fit is cut at the capacity and continues in the next
+// bin.  False when more than n_bins bins are needed.
+static bool stream_bins(const std::vector<std::pair<int, int>> &bt, double cap, int n_bins, Bins &bins) {
+    std::vector<int> order(bt.size());
+    for (size_t i = 0; i < order.size(); ++i) order[i] = (int)i;
+    std::stable_sort(order.begin(), order.end(), [&](int x, int y) {
+        return bt[x].second - bt[x].first > bt[y].second - bt[y].first;
+    });
+    std::vector<int> seq;
+    for (int i = 0, j = (int)order.size() - 1; i <= j;) {
+        seq.push_back(order[i++]);
+        if (i <= j) seq.push_back(order[j--]);
+    }
+    bins.assign(1, {});
+    double load = 0.0;
+    for (int b : seq) {
+        int lo = bt[b].first;
+        const int hi = bt[b].second;
+        while (lo < hi) {
+            const int rem = hi - lo;
+            const double room = cap - load - kUnitCost;
+            const bool empty = bins.back().empty();
+            // An empty bin takes any remainder up to a minimum piece whole.
+            if (rem <= room || (empty && rem <= kMinUnitTiles)) {
+                bins.back().push_back({b, lo, hi});
+                load += rem + kUnitCost;
+                break;
+            }
+            // The tiles that fit, leaving at least a minimum piece behind
+            // (rem > kMinUnitTiles here when the bin is empty, so an empty
+            // bin always takes at least one tile and every pass progresses).
+            int take = std::max(0, (int)room);
+            if (rem - take < kMinUnitTiles) take = rem - kMinUnitTiles;
+            if (empty) take = std::max(take, 1);
+            if (take >= kMinUnitTiles || (empty && take >= 1)) {
+                bins.back().push_back({b, lo, lo + take});
+                lo += take;
+            }
+            if (lo < hi) {
+                if ((int)bins.size() == n_bins) return false;
+                bins.push_back({});
+                load = 0.0;
+            }
+        }
+    }
+    return true;
+}
+
+// The cheaper of the two schedules (by the cost model): fixed-length units
+// placed by LPT (16 .. 128 tiles, or longer when a block needs it to stay
+// within kPrefillMaxUnits units), or stream-K packing at the smallest
+// feasible capacity or a little above.  Stream-K wins on causal prompts
+// (every CU gets the same number of tiles, with about one split per CU);
+// LPT wins where few long blocks each need many pieces.
+static int build_schedule(const std::vector<std::pair<int, int>> &bt, int n_bins, int head_dim, Bins &best) {
     int max_tiles = 1;
-    for (auto &bt : block_tiles) max_tiles = std::max(max_tiles, bt.second - bt.first);
-    int best = -1;
-    double best_cost = 0.0;
-    std::vector<double> load;
-    std::vector<int> lens;
-    // Candidates: 16 .. 128 tiles, or longer when a block needs it to stay
-    // within kPrefillMaxUnits units.
+    long long total = 0;
+    for (auto &x : bt) {
+        max_tiles = std::max(max_tiles, x.second - x.first);
+        total += x.second - x.first;
+    }
+    double best_cost = -1.0;
+    auto consider = [&](Bins &&bins) {
+        const double cost = schedule_cost(bins, (int)bt.size(), head_dim);
+        if (cost >= 0.0 && (best_cost < 0.0 || cost < best_cost)) {
+            best_cost = cost;
+            best = std::move(bins);
+        }
+    };
     const int ut_hi = std::max(128, ((max_tiles + kPrefillMaxUnits - 1) / kPrefillMaxUnits + 7) / 8 * 8);
     for (int ut = ut_hi; ut >= 16; ut -= 8) {
         if ((max_tiles + ut - 1) / ut > kPrefillMaxUnits) break;
-        lens.clear();
-        bool split = false;
-        for (auto &bt : block_tiles) {
-            const int tiles = bt.second - bt.first, nu = (tiles + ut - 1) / ut;
-            split |= nu > 1;
-            for (int j = 0; j < nu; ++j) lens.push_back((j + 1) * tiles / nu - j * tiles / nu);
-        }
-        std::sort(lens.begin(), lens.end(), std::greater<int>());
-        load.assign((size_t)std::max(1, num_cus), 0.0);
-        std::make_heap(load.begin(), load.end(), std::greater<double>());
-        for (int len : lens) {
-            std::pop_heap(load.begin(), load.end(), std::greater<double>());
-            load.back() += len + 1.5;
-            std::push_heap(load.begin(), load.end(), std::greater<double>());
-        }
-        const double cost = *std::max_element(load.begin(), load.end()) + (split ? 3.0 : 0.0);
-        if (best < 0 || cost < best_cost) {
-            best = ut;
-            best_cost = cost;
-        }
+        consider(lpt_bins(bt, ut, n_bins));
     }
-    return best;
+    double lo = (double)total / n_bins + kUnitCost, hi = lo + max_tiles + 2 * kUnitCost;
+    Bins bins;
+    if (stream_bins(bt, hi, n_bins, bins)) {
+        while (hi - lo > 0.25) {
+            const double mid = 0.5 * (lo + hi);
+            if (stream_bins(bt, mid, n_bins, bins))
+                hi = mid;
+            else
+                lo = mid;
+        }
+        for (int k = 0; k < 12; ++k)
+            if (stream_bins(bt, hi + 0.5 * k, n_bins, bins)) consider(std::move(bins));
+    }
+    return best_cost < 0.0 ? -1 : 0;
 }
 
-// The unit table of a's shape: cached, or built and uploaded (synchronously:
-// graph capture needs an earlier call with the same shape).
+// The unit table, workgroup ranges and block table of a schedule; checks
+// that every block's pieces tile its range exactly.
+static int schedule_tables(const std::vector<std::pair<int, int>> &bt, Bins &bins, std::vector<PrefillUnit> &units,
+                           std::vector<int> &bin_start, std::vector<PrefillBlockInfo> &blocks, int &n_slots) {
+    const int n_blocks = (int)bt.size();
+    bins.erase(std::remove_if(bins.begin(), bins.end(), [](const std::vector<Piece> &x) { return x.empty(); }),
+               bins.end());
+    std::stable_sort(bins.begin(), bins.end(), [](const std::vector<Piece> &x, const std::vector<Piece> &y) {
+        int lx = 0, ly = 0;
+        for (auto &pc : x) lx += pc[2] - pc[1];
+        for (auto &pc : y) ly += pc[2] - pc[1];
+        return lx > ly;
+    });
+    std::vector<std::vector<std::pair<int, int>>> of_block(n_blocks);  // (t_lo, unit index)
+    units.clear();
+    bin_start.assign(1, 0);
+    for (auto &bin : bins) {
+        for (auto &pc : bin) {
+            of_block[pc[0]].push_back({pc[1], (int)units.size()});
+            units.push_back({pc[0], pc[1], pc[2], -1});
+        }
+        bin_start.push_back((int)units.size());
+    }
+    blocks.assign(n_blocks, {0, 0});
+    n_slots = 0;
+    for (int b = 0; b < n_blocks; ++b) {
+        auto &v = of_block[b];
+        std::sort(v.begin(), v.end());
+        int t = bt[b].first;
+        for (auto &x : v) {
+            const PrefillUnit &u = units[x.second];
+            if (u.t_lo != t || u.t_hi <= u.t_lo) return set_error(G4_ERR_COMPUTE, "prefill schedule does not tile a block");
+            t = u.t_hi;
+        }
+        if (t != bt[b].second || v.empty() || (int)v.size() > kPrefillMaxUnits)
+            return set_error(G4_ERR_COMPUTE, "prefill schedule does not tile a block");
+        blocks[b] = {v.size() > 1 ? n_slots : 0, (int)v.size()};
+        if (v.size() > 1)
+            for (auto &x : v) units[x.second].slot = n_slots++;
+    }
+    return G4_OK;
+}
+
+// [t_lo, t_hi) tiles of each position block of a prefill shape.
+static std::vector<std::pair<int, int>> block_tile_ranges(int64_t pos0, int64_t N, int64_t window) {
+    const int n_blocks = (int)((N + kPosPerBlock - 1) / kPosPerBlock);
+    const int64_t last_pos = pos0 + N - 1;
+    std::vector<std::pair<int, int>> bt(n_blocks);
+    for (int b = 0; b < n_blocks; ++b) {
+        const int64_t P0 = pos0 + (int64_t)kPosPerBlock * b;
+        const int64_t P1 = std::min<int64_t>(P0 + kPosPerBlock - 1, last_pos);
+        const int64_t k_lo = (window > 0 && P0 + 1 > window) ? P0 + 1 - window : 0;
+        bt[b] = {(int)(k_lo / 16), (int)(P1 / 16 + 1)};
+    }
+    return bt;
+}
+
+static int bins_for(int num_cus, int n_kv_heads) { return std::max(1, num_cus / std::max(1, n_kv_heads)); }
+
+// The schedule tables of a's shape: cached, or built and uploaded
+// (synchronously: graph capture needs an earlier call with the same shape).
 static int plan_for(g4_ctx *ctx, const PrefillArgs &a, const PrefillPlan **out) {
     PrefillPlans &ps = plans_of(ctx);
     ++ps.tick;
     for (auto &pl : ps.plans)
-        if (pl.pos0 == a.pos0 && pl.N == a.N && pl.window == a.window && pl.head_dim == a.head_dim) {
+        if (pl.pos0 == a.pos0 && pl.N == a.N && pl.window == a.window && pl.head_dim == a.head_dim &&
+            pl.n_kv_heads == a.n_kv_heads) {
             pl.last_use = ps.tick;
             *out = &pl;
             return G4_OK;
         }
-    const int n_blocks = (int)((a.N + kPosPerBlock - 1) / kPosPerBlock);
-    const int64_t last_pos = a.pos0 + a.N - 1;
-    std::vector<std::pair<int, int>> block_tiles(n_blocks);  // [t_lo, t_hi) per position block
-    for (int b = 0; b < n_blocks; ++b) {
-        const int64_t P0 = a.pos0 + (int64_t)kPosPerBlock * b;
-        const int64_t P1 = std::min<int64_t>(P0 + kPosPerBlock - 1, last_pos);
-        const int64_t k_lo = (a.window > 0 && P0 + 1 > a.window) ? P0 + 1 - a.window : 0;
-        block_tiles[b] = {(int)(k_lo / 16), (int)(P1 / 16 + 1)};
-    }
-    const int unit_tiles = choose_unit_tiles(block_tiles, ctx->num_cus);
-    if (unit_tiles < 0) return set_error(G4_ERR_COMPUTE, "prefill key range too long for one call");
+    const std::vector<std::pair<int, int>> bt = block_tile_ranges(a.pos0, a.N, a.window);
+    Bins bins;
+    if (build_schedule(bt, bins_for(ctx->num_cus, a.n_kv_heads), a.head_dim, bins) != 0)
+        return set_error(G4_ERR_COMPUTE, "prefill key range too long for one call");
     std::vector<PrefillUnit> units;
-    std::vector<PrefillBlockInfo> blocks(n_blocks);
+    std::vector<int> bin_start;
+    std::vector<PrefillBlockInfo> blocks;
     int n_slots = 0;
-    for (int b = 0; b < n_blocks; ++b) {
-        const int t_lo = block_tiles[b].first, tiles = block_tiles[b].second - t_lo;
-        const int nu = (tiles + unit_tiles - 1) / unit_tiles;
-        blocks[b] = {nu > 1 ? n_slots : 0, nu};
-        for (int j = 0; j < nu; ++j) {
-            const int lo = t_lo + j * tiles / nu, hi = t_lo + (j + 1) * tiles / nu;
-            units.push_back({b, lo, hi, nu > 1 ? n_slots + j : -1});
-        }
-        if (nu > 1) n_slots += nu;
-    }
-    // Heaviest units first: the hardware dispatches workgroups in order.
-    std::stable_sort(units.begin(), units.end(), [](const PrefillUnit &x, const PrefillUnit &y) {
-        return (x.t_hi - x.t_lo) > (y.t_hi - y.t_lo);
-    });
+    int rc = schedule_tables(bt, bins, units, bin_start, blocks, n_slots);
+    if (rc != G4_OK) return rc;
     PrefillPlan pl;
     pl.pos0 = a.pos0;
     pl.N = a.N;
     pl.window = a.window;
     pl.head_dim = a.head_dim;
-    pl.unit_tiles = unit_tiles;
+    pl.n_kv_heads = a.n_kv_heads;
     pl.n_units = (int)units.size();
-    pl.n_blocks = n_blocks;
+    pl.n_bins = (int)bin_start.size() - 1;
+    pl.n_blocks = (int)blocks.size();
     pl.n_slots = n_slots;
     pl.last_use = ps.tick;
     hipError_t e = hipMalloc(&pl.units, units.size() * sizeof(PrefillUnit));
+    if (e == hipSuccess) e = hipMalloc(&pl.bin_start, bin_start.size() * sizeof(int));
     if (e == hipSuccess) e = hipMalloc(&pl.blocks, blocks.size() * sizeof(PrefillBlockInfo));
     if (e == hipSuccess)
         e = hipMemcpy(pl.units, units.data(), units.size() * sizeof(PrefillUnit), hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+        e = hipMemcpy(pl.bin_start, bin_start.data(), bin_start.size() * sizeof(int), hipMemcpyHostToDevice);
     if (e == hipSuccess)
         e = hipMemcpy(pl.blocks, blocks.data(), blocks.size() * sizeof(PrefillBlockInfo), hipMemcpyHostToDevice);
     if (e != hipSuccess) {
@@ -602,6 +791,34 @@ static int plan_for(g4_ctx *ctx, const PrefillArgs &a, const PrefillPlan **out) 
         ps.plans.push_back(pl);
         *out = &ps.plans.back();
     }
+    return G4_OK;
+}
+
+int describe_prefill_schedule(int64_t pos0, int64_t N, int64_t window, int head_dim, int n_kv_heads, int num_cus,
+                              int32_t *units4, int64_t units_cap, int32_t *bin_start_out, int64_t bins_cap,
+                              int32_t *counts) {
+    const std::vector<std::pair<int, int>> bt = block_tile_ranges(pos0, N, window);
+    Bins bins;
+    if (build_schedule(bt, bins_for(num_cus, n_kv_heads), head_dim, bins) != 0)
+        return set_error(G4_ERR_COMPUTE, "prefill key range too long for one call");
+    std::vector<PrefillUnit> units;
+    std::vector<int> bin_start;
+    std::vector<PrefillBlockInfo> blocks;
+    int n_slots = 0;
+    int rc = schedule_tables(bt, bins, units, bin_start, blocks, n_slots);
+    if (rc != G4_OK) return rc;
+    counts[0] = (int32_t)units.size();
+    counts[1] = (int32_t)bin_start.size() - 1;
+    counts[2] = n_slots;
+    if ((int64_t)units.size() > units_cap || (int64_t)bin_start.size() > bins_cap)
+        return set_error(G4_ERR_MSG, "prefill schedule: output arrays too small");
+    for (size_t i = 0; i < units.size(); ++i) {
+        units4[4 * i] = units[i].block;
+        units4[4 * i + 1] = units[i].t_lo;
+        units4[4 * i + 2] = units[i].t_hi;
+        units4[4 * i + 3] = units[i].slot;
+    }
+    for (size_t i = 0; i < bin_start.size(); ++i) bin_start_out[i] = bin_start[i];
     return G4_OK;
 }
 
@@ -646,6 +863,7 @@ int launch_prefill(g4_ctx *ctx, const PrefillArgs &a, hipStream_t stream) {
     p.scale = a.scale;
     p.out = a.out;
     p.units = pl.units;
+    p.bin_start = pl.bin_start;
     p.blocks = pl.blocks;
     p.n_slots = pl.n_slots;
     p.status = ctx->status_dev;
@@ -659,7 +877,7 @@ int launch_prefill(g4_ctx *ctx, const PrefillArgs &a, hipStream_t stream) {
         p.part_o = (float *)ctx->ws.ptr;
         p.part_ml = (float2 *)((char *)ctx->ws.ptr + (obytes + 255) / 256 * 256);
     }
-    dim3 grid((unsigned)pl.n_units, (unsigned)a.n_kv_heads);
+    dim3 grid((unsigned)pl.n_bins, (unsigned)a.n_kv_heads);
     if (D == 256)
         hipLaunchKernelGGL(prefill_kernel<256>, grid, dim3(PrefillShape<256>::THREADS), 0, stream, p);
     else

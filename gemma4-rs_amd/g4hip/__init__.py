@@ -87,6 +87,7 @@ _SIGS = {
     "g4_logits_q8_0": (c_int, [c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_f32, c_vp, c_vp]),
     "g4_matvec_bf16": (c_int, [c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp]),
     "g4_matvec_f32": (c_int, [c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp]),
+    "g4_prefill_schedule": (c_int, [c_i64, c_i64, c_i64, c_int, c_int, c_int, c_vp, c_i64, c_vp, c_i64, c_vp]),
     "g4_layer_is_global": (c_int, [c_int, c_int]),
     "g4_kv_source_layer": (c_int, [c_int, c_int, c_int, ctypes.POINTER(c_int)]),
     "g4_windowed_len": (None, [c_i64, c_i64, ctypes.POINTER(c_i64), ctypes.POINTER(c_i64)]),
@@ -183,6 +184,25 @@ def proportional_rope_freq_factors(head_dim, p):
 
 
 # ------------------------------------------------------------------- context
+def prefill_schedule(pos0, N, window, head_dim, n_kv_heads=1, num_cus=256):
+    """g4_prefill_schedule: (units, bin_start) of the prefill kernel for a
+    shape, as int32 numpy arrays -- units[i] = (block, t_lo, t_hi, slot),
+    workgroup w runs units[bin_start[w]:bin_start[w+1]].  Host only."""
+    import numpy as np
+    counts = np.zeros(3, np.int32)
+    units = np.zeros((1, 4), np.int32)
+    bins = np.zeros(1, np.int32)
+    code = lib().g4_prefill_schedule(pos0, N, window, head_dim, n_kv_heads, num_cus, units.ctypes.data, 1,
+                                     bins.ctypes.data, 1, counts.ctypes.data)
+    if code not in (0, 5):
+        _raise(code)
+    units = np.zeros((max(1, int(counts[0])), 4), np.int32)
+    bins = np.zeros(int(counts[1]) + 1, np.int32)
+    _raise(lib().g4_prefill_schedule(pos0, N, window, head_dim, n_kv_heads, num_cus, units.ctypes.data,
+                                     len(units), bins.ctypes.data, len(bins), counts.ctypes.data))
+    return units[:int(counts[0])], bins
+
+
 class Context:
     """One device's backend context (g4_ctx)."""
 

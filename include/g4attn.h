@@ -109,6 +109,20 @@ int g4_attend_prefill(g4_ctx *ctx, const float *q_dev, const float *k_cache_dev,
                       int64_t window, int n_heads, int n_kv_heads, int head_dim, float scale,
                       float *out_dev, g4_stream stream);
 
+/* Work schedule of g4_attend_prefill's MFMA path (head_dim 256 or 512,
+ * 8 query heads per KV head) on a GPU with num_cus compute units: position
+ * blocks of 8 queries are cut into units of 16-key tiles, and workgroup w
+ * (of n_bins per KV head) runs units bin_start[w] .. bin_start[w+1]-1 in
+ * turn.  units (host) gets 4 int32 per unit: {block, first tile, end tile,
+ * partial slot or -1 for a block computed by one unit}; bin_start (host)
+ * n_bins+1 entries; counts (host) {n_units, n_bins, n_slots}.  Host only,
+ * no device work; counts are filled even when the arrays are too small
+ * (then G4_ERR_MSG).  No counterpart in the reference, whose prompt runs
+ * token at a time (crates/llm-gemma4/src/impl_/generate.rs:37-41). */
+int g4_prefill_schedule(int64_t pos0, int64_t N, int64_t window, int head_dim, int n_kv_heads, int num_cus,
+                        int32_t *units, int64_t units_cap, int32_t *bin_start, int64_t bins_cap,
+                        int32_t *counts);
+
 /* ----------------------------------------- attention input preparation */
 /* rms_norm (crates/llm-backend-cpu/src/ops.rs:45-56) applied to each of
  * n_rows rows of `width` floats (norm_heads, model.rs:283-290): f64 mean of
