@@ -174,6 +174,12 @@ def bench_stack(ctx, torch, prep, g4hip, steps, warmup, ctx_len=8192):
 
 
 def bench_prefill(ctx, torch, prep, steps, warmup, N=2048):
+    """Causal prefill of an N-token prompt through one sliding and one global
+    layer.  The timed steps replay as one captured graph (a graph per step
+    adds a launch gap of about 4 us to each 0.1-0.4 ms step), after
+    `warmup` untimed steps: the clocks need tens of milliseconds of this
+    load to settle (global layer 348 us after 2 warm-up steps, 322 us after
+    50, measured in one process)."""
     res = {}
     total_flops, total_s = 0, 0.0
     for name, d, window, base in (("sliding_d256_W512", 256, WINDOW, LOCAL_BASE), ("global_d512", 512, 0, GLOBAL_BASE)):
@@ -183,7 +189,7 @@ def bench_prefill(ctx, torch, prep, steps, warmup, N=2048):
         q = prep.rows(N, d, 0, base, freqs, heads=N_HEADS)
         out = torch.zeros(N * N_HEADS * d, device="cuda")
         wall, ev = time_steps(torch, lambda i: ctx.attend_prefill(q, K, V, 0, N, window, N_HEADS, N_KV, d, out),
-                              steps, warmup)
+                              steps, warmup, block=steps)
         ctx.check_status()
         fl = prefill_flops(N, window, d)
         res[name] = {"us": ev / steps * 1e6, "tflops": fl / (ev / steps) / 1e12, "flops": fl}
@@ -237,7 +243,7 @@ def bench_layer_steps(ctx, torch, prep, steps, warmup, T=4096, N=2048):
                             row_stride=N_KV * d)
             ctx.attend_prefill(q, Kc, Vc, 0, N, window, N_HEADS, N_KV, d, out)
 
-        wall, ev = time_steps(torch, pstep, psteps, 2)
+        wall, ev = time_steps(torch, pstep, psteps, max(2, warmup // 4), block=psteps)
         ctx.check_status()
         fl = prefill_flops(N, window, d)
         res[f"prefill_2048_{name}_layer"] = {"us": ev / psteps * 1e6, "tflops": fl / (ev / psteps) / 1e12}
@@ -385,7 +391,7 @@ def main():
             fn = {"global": lambda: bench_global_decode(ctx, torch, prep, args.steps, args.warmup),
                   "sliding": lambda: bench_sliding_decode(ctx, torch, prep, args.steps, args.warmup),
                   "stack": lambda: bench_stack(ctx, torch, prep, g4hip, k, 5),
-                  "prefill": lambda: bench_prefill(ctx, torch, prep, max(5, k // 10), 2),
+                  "prefill": lambda: bench_prefill(ctx, torch, prep, max(5, k // 10), args.warmup),
                   "ragged": lambda: bench_ragged(ctx, torch, prep, max(5, k // 4), 2),
                   "layer": lambda: bench_layer_steps(ctx, torch, prep, args.steps, args.warmup),
                   "matvec": lambda: bench_matvec(ctx, torch, max(20, k // 2), 5),
@@ -404,7 +410,7 @@ def main():
             k = max(20, args.steps // 4)
             workloads["sliding_decode_d256_ctx64"] = bench_sliding_decode(ctx, torch, prep, args.steps, args.warmup)
             workloads["e2b_stack_35_layers_ctx8192"] = bench_stack(ctx, torch, prep, g4hip, k, 5)
-            workloads["prefill_2048"] = bench_prefill(ctx, torch, prep, max(5, k // 10), 2)
+            workloads["prefill_2048"] = bench_prefill(ctx, torch, prep, max(5, k // 10), args.warmup)
             workloads["ragged_decode_B32"] = bench_ragged(ctx, torch, prep, max(5, k // 4), 2)
             workloads["layer_drivers"] = bench_layer_steps(ctx, torch, prep, args.steps, args.warmup)
             workloads["q8_0_matvec"] = bench_matvec(ctx, torch, max(20, k // 2), 5)
