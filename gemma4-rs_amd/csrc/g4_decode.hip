@@ -220,6 +220,14 @@ constexpr int kBufferWord3 = 0x00020000;
 // Cache-policy operand of a buffer store: SC1, device scope -- the store is
 // written through the XCD's L2 to the point of coherence.
 constexpr int kDeviceScope = 16;
+// Cache-policy operand of a buffer load: NT, non-temporal (streamed, not kept
+// for reuse).  A single sequence split over many workgroups reads K/V with it
+// (4096 keys from HBM: 11.23 -> 10.93 us; 512 keys: 8.12 -> 7.59 us): its
+// rows are read once per step.  Batches, unsplit sequences and the ragged
+// stream kernel read with the default policy: when their rows are still
+// cached from the previous step, NT loads were slower (a 32-sequence sliding
+// batch 21.1 -> 23.1 us, 64 keys 6.75 -> 6.88 us, the stream kernel 4%).
+constexpr int kNonTemporal = 2;
 
 // A wavefront's view of one (sequence, KV head) decode: lane (g, c) =
 // (lane/16, lane%16) of wave w, which owns head dims [base, base + DW).
@@ -262,18 +270,19 @@ struct DecodeLane {
     // The tile offset goes into the per-lane offset: the hardware range
     // check covers that offset (not the scalar one), so every row at or past
     // the end -- in the last tile, or a whole tile past it -- reads 0.
+    template <int AUX>
     __device__ __forceinline__ void load_tile(__amdgpu_buffer_rsrc_t krs, __amdgpu_buffer_rsrc_t vrs, int tile,
                                               KvTile<D> &T) const {
         const uint32_t toff = (uint32_t)tile * tile_bytes;
 #pragma unroll
         for (int u = 0; u < KU; ++u)
-            T.k[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, koff + toff + 64u * u, 0, 0));
+            T.k[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, koff + toff + 64u * u, 0, AUX));
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             if constexpr (TW == 4)
-                T.v[r] = __builtin_bit_cast(VRow, __builtin_amdgcn_raw_buffer_load_b128(vrs, voff[r] + toff, 0, 0));
+                T.v[r] = __builtin_bit_cast(VRow, __builtin_amdgcn_raw_buffer_load_b128(vrs, voff[r] + toff, 0, AUX));
             else
-                T.v[r] = __builtin_bit_cast(VRow, __builtin_amdgcn_raw_buffer_load_b64(vrs, voff[r] + toff, 0, 0));
+                T.v[r] = __builtin_bit_cast(VRow, __builtin_amdgcn_raw_buffer_load_b64(vrs, voff[r] + toff, 0, AUX));
         }
     }
 };
@@ -434,21 +443,21 @@ struct DecodeAcc {
 // unconditionally (clamped to the last pair), so the compiler's wait counts
 // stay exact and never wait on a prefetch.  A pair's second tile past the
 // end (odd tile count) reads zeros and is masked.
-template <int D, int NBUF>
+template <int D, int NBUF, int AUX>
 __device__ __forceinline__ void run_pairs(const DecodeLane<D> &ln, DecodeAcc<D> &acc, __amdgpu_buffer_rsrc_t krs,
                                           __amdgpu_buffer_rsrc_t vrs, int q_first, int n_pairs, int n_keys,
                                           float scale, PairScores<D> &sx, int &buf) {
     constexpr int NPAIR = NBUF / 2;
     KvTile<D> T[NPAIR][2];
     if (n_keys - 32 * q_first <= 16) {  // a single tile: its second half is not computed
-        ln.load_tile(krs, vrs, 2 * q_first, T[0][0]);
+        ln.template load_tile<AUX>(krs, vrs, 2 * q_first, T[0][0]);
         acc.template pair<1>(ln, T[0], n_keys - 32 * q_first, scale, sx, buf);
         return;
     }
     auto load_pair = [&](int i, KvTile<D> (&P)[2]) {
         const int q = q_first + (i < n_pairs ? i : n_pairs - 1);
-        ln.load_tile(krs, vrs, 2 * q, P[0]);
-        ln.load_tile(krs, vrs, 2 * q + 1, P[1]);
+        ln.template load_tile<AUX>(krs, vrs, 2 * q, P[0]);
+        ln.template load_tile<AUX>(krs, vrs, 2 * q + 1, P[1]);
     };
 #pragma unroll
     for (int b = 0; b < NPAIR - 1; ++b) load_pair(b, T[b]);
@@ -470,7 +479,7 @@ __device__ __forceinline__ void run_pairs(const DecodeLane<D> &ln, DecodeAcc<D> 
 
 // One workgroup = one (split, KV head, sequence); NW wavefronts, each owning
 // DW = D/NW of the head dims.
-template <int D, int MODE, int NBUF>
+template <int D, int MODE, int NBUF, int AUX>
 __global__ __launch_bounds__(64 * DecodeShape<D>::NW) void decode_split_kernel(DecodeK p) {
     const int split = blockIdx.x, kvh = blockIdx.y, s = blockIdx.z;
     const DecodeLane<D> ln((int)p.row_stride);
@@ -504,7 +513,7 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::NW) void decode_split_kernel(D
     acc.start(ln, p.q + ((int64_t)s * p.n_heads + head) * D, col_valid);
     __shared__ PairScores<D> sx;
     int buf = 0;
-    run_pairs<D, NBUF>(ln, acc, krs, vrs, 0, n_pairs, n_keys, p.scale, sx, buf);
+    run_pairs<D, NBUF, AUX>(ln, acc, krs, vrs, 0, n_pairs, n_keys, p.scale, sx, buf);
 
     if (ln.wave == 0 && __any(acc.bad && col_valid) && ln.lane == 0) atomicOr(p.status, kStatusNonFinite);
     if (n_splits == 1) {
@@ -607,7 +616,7 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::NW) void decode_stream_kernel(
         const __amdgpu_buffer_rsrc_t krs = ln.rows(p.k + first, n_keys, stride);
         const __amdgpu_buffer_rsrc_t vrs = ln.rows(p.v + first, n_keys, stride);
         acc.start(ln, p.q + ((int64_t)cs * p.n_heads + head) * D, col_valid);
-        run_pairs<D, NBUF>(ln, acc, krs, vrs, g - ga, ge - g, n_keys, p.scale, sx, buf);
+        run_pairs<D, NBUF, 0>(ln, acc, krs, vrs, g - ga, ge - g, n_keys, p.scale, sx, buf);
         if (g == ga && ge == gb) {
             acc.write_output(ln, p.out + ((int64_t)cs * p.n_heads + head) * D, col_valid, p.status);
         } else {  // slot 0: the run's first sequence; 1: its last
@@ -868,12 +877,22 @@ int launch_mode(g4_ctx *ctx, const DecodeArgs &a, DecodeK p, hipStream_t stream)
         p.part_ml = (float2 *)((char *)ctx->ws.ptr + off);
     }
     dim3 grid((unsigned)max_splits, (unsigned)a.n_kv_heads, (unsigned)a.B);
-    if (D == 256)
-        hipLaunchKernelGGL((decode_split_kernel<256, MODE, kDecodeBuffers>), grid,
-                           dim3(64 * DecodeShape<256>::NW), 0, stream, p);
-    else
-        hipLaunchKernelGGL((decode_split_kernel<512, MODE, kDecodeBuffers>), grid,
-                           dim3(64 * DecodeShape<512>::NW), 0, stream, p);
+    const bool stream_kv = MODE == kSingle && max_splits > 1;  // K/V read once per step: NT loads
+    if (D == 256) {
+        if (stream_kv)
+            hipLaunchKernelGGL((decode_split_kernel<256, MODE, kDecodeBuffers, kNonTemporal>), grid,
+                               dim3(64 * DecodeShape<256>::NW), 0, stream, p);
+        else
+            hipLaunchKernelGGL((decode_split_kernel<256, MODE, kDecodeBuffers, 0>), grid,
+                               dim3(64 * DecodeShape<256>::NW), 0, stream, p);
+    } else {
+        if (stream_kv)
+            hipLaunchKernelGGL((decode_split_kernel<512, MODE, kDecodeBuffers, kNonTemporal>), grid,
+                               dim3(64 * DecodeShape<512>::NW), 0, stream, p);
+        else
+            hipLaunchKernelGGL((decode_split_kernel<512, MODE, kDecodeBuffers, 0>), grid,
+                               dim3(64 * DecodeShape<512>::NW), 0, stream, p);
+    }
     G4_HIP(hipGetLastError());
     if (max_splits > 1) {
         const dim3 mgrid(D * group / 64, a.n_kv_heads, a.B);

@@ -36,11 +36,18 @@ constexpr int kQ8Bytes = 34;   // f16 scale + 32 int8
 constexpr int kBufferWord3 = 0x00020000;
 constexpr int kVmcntZero = 0x0F70;  // s_waitcnt vmcnt(0), other counters untouched
 
+// Cache-policy operand of a buffer load: NT, non-temporal.  Large matrices
+// stream their weights with it (output head 84.6 -> 78.9 us); small ones,
+// which stay latency-bound, were 0.6 us slower with it.
+constexpr int kNonTemporal = 2;
+
 // One 16-byte load per active lane from `rsrc` at byte offset voff, written
-// straight to LDS at lds + 16 * lane (lds is the same for the whole wavefront).
+// straight to LDS at lds + 16 * lane (lds is the same for the whole
+// wavefront); AUX is the cache policy.
+template <int AUX>
 __device__ inline void load_to_lds(__amdgpu_buffer_rsrc_t rsrc, u32x4 *lds, uint32_t voff) {
 #if defined(__HIP_DEVICE_COMPILE__)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void *)lds, 16, voff, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void *)lds, 16, voff, 0, 0, AUX);
 #endif
 }
 
@@ -125,7 +132,7 @@ enum Epilogue : int { kPlain = 0, kSoftcap = 1, kGeglu = 2, kGegluFp16 = 3 };
 // (up) beside the first (gate).  Large matrices stage one row at a time in
 // small workgroups, so that many are resident per CU (measured faster than
 // double-buffering fewer of them); small ones stage all their rows at once.
-template <int EPI, int NS>
+template <int EPI, int NS, bool STREAM>
 __global__ __launch_bounds__(64) void matvec_q8_0_kernel(const unsigned char *__restrict__ w,
                                                          const unsigned char *__restrict__ w2, int64_t rows,
                                                          int nb, const float *__restrict__ xs,
@@ -173,7 +180,8 @@ __global__ __launch_bounds__(64) void matvec_q8_0_kernel(const unsigned char *__
                     (void *)((m == 0 ? w : w2) + (row0 + r0 + r) * row_len), 0, row_len, kBufferWord3);
                 u32x4 *dst = stage + (r * NM + m) * chunks;
                 for (int k = 0; k * 64 < chunks; ++k)
-                    if (k * 64 + lane < chunks) load_to_lds(rs, dst + 64 * k, (uint32_t)(k * 64 + lane) * 16u);
+                    if (k * 64 + lane < chunks)
+                        load_to_lds<STREAM ? kNonTemporal : 0>(rs, dst + 64 * k, (uint32_t)(k * 64 + lane) * 16u);
             }
         __builtin_amdgcn_s_waitcnt(kVmcntZero);
         __syncthreads();
@@ -343,13 +351,13 @@ __global__ __launch_bounds__(256) void matvec_f32_kernel(const float *__restrict
     out[row] = sum;
 }
 
-template <int EPI, int NS>
+template <int EPI, int NS, bool STREAM>
 int launch_q8_rows(const MatvecArgs &a, int g, int rb, hipStream_t stream) {
     constexpr int NM = EPI >= kGeglu ? 2 : 1;
     const int nb = (int)(a.cols / kQ8Values);
     const size_t lds = (size_t)g * NM * (nb * kQ8Bytes) + (size_t)NM * rb * (nb + 1) * sizeof(float);
     const int64_t groups = (a.rows + rb - 1) / rb;
-    hipLaunchKernelGGL((matvec_q8_0_kernel<EPI, NS>), dim3((unsigned)groups), dim3(64), lds, stream, a.w, a.w2,
+    hipLaunchKernelGGL((matvec_q8_0_kernel<EPI, NS, STREAM>), dim3((unsigned)groups), dim3(64), lds, stream, a.w, a.w2,
                        a.rows, nb, a.xs, (const int *)a.xq, a.xs ? nullptr : a.x, a.arg, g, rb, a.out);
     G4_HIP(hipGetLastError());
     return G4_OK;
@@ -395,11 +403,19 @@ int launch_q8(g4_ctx *ctx, MatvecArgs a, hipStream_t stream) {
             g = rb;
         }
         const int ns = (int)((nb + 63) / 64);
+        if (large) {
+            switch (ns) {
+            case 1: return launch_q8_rows<EPI, 1, true>(a, (int)g, (int)rb, stream);
+            case 2: return launch_q8_rows<EPI, 2, true>(a, (int)g, (int)rb, stream);
+            case 3: return launch_q8_rows<EPI, 3, true>(a, (int)g, (int)rb, stream);
+            default: return launch_q8_rows<EPI, 4, true>(a, (int)g, (int)rb, stream);
+            }
+        }
         switch (ns) {
-        case 1: return launch_q8_rows<EPI, 1>(a, (int)g, (int)rb, stream);
-        case 2: return launch_q8_rows<EPI, 2>(a, (int)g, (int)rb, stream);
-        case 3: return launch_q8_rows<EPI, 3>(a, (int)g, (int)rb, stream);
-        default: return launch_q8_rows<EPI, 4>(a, (int)g, (int)rb, stream);
+        case 1: return launch_q8_rows<EPI, 1, false>(a, (int)g, (int)rb, stream);
+        case 2: return launch_q8_rows<EPI, 2, false>(a, (int)g, (int)rb, stream);
+        case 3: return launch_q8_rows<EPI, 3, false>(a, (int)g, (int)rb, stream);
+        default: return launch_q8_rows<EPI, 4, false>(a, (int)g, (int)rb, stream);
         }
     }
     hipLaunchKernelGGL((matvec_q8_0_rowwise_kernel<EPI>), dim3((unsigned)((a.rows + 255) / 256)), dim3(256), 0,
