@@ -389,15 +389,17 @@ int launch_q8(g4_ctx *ctx, MatvecArgs a, hipStream_t stream) {
         if (rq != G4_OK) return rq;
     }
     if (fast) {
-        // Large matrices: rb_max rows per workgroup, staged one at a time,
-        // so that the workgroups are small and many are resident per CU
-        // (measured faster than staging or double-buffering more rows in
-        // fewer of them).  Small ones: a workgroup's rows all in flight at
-        // once, and about eight workgroups per CU.
+        // Large matrices: 8 rows per workgroup, staged two at a time, so
+        // that the workgroups are small and many are resident per CU, each
+        // with two rows in flight.  Output head (262,144 x 1536, quantize
+        // included): 75.5 us with 16 rows staged one at a time, 71.5 with
+        // 8 (or 4) staged two at a time, 87 with 8 staged eight at a time,
+        // 97-142 with 64 rows per workgroup.  Small ones: a workgroup's rows
+        // all in flight at once, and about eight workgroups per CU.
         int64_t rb, g;
         if (large) {
-            rb = rb_max;
-            g = 1;
+            rb = std::min<int64_t>(8, rb_max);
+            g = std::min<int64_t>(2, rb);
         } else {
             rb = std::max<int64_t>(1, std::min<int64_t>(rb_max, a.rows / (8LL * num_cus)));
             g = rb;
