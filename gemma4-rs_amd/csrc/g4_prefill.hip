@@ -441,7 +441,8 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillK p) {
         const int g = lane >> 4, c = lane & 15;
         f32x4 v[kPrefillMaxUnitsDev];
 #pragma unroll
-        for (int j = 0; j < kPrefillMaxUnitsDev; ++j) v[j] = base[(j < n ? j : 0) * slot_stride + e];
+        for (int j = 0; j < kPrefillMaxUnitsDev; ++j)  // n is uniform: scalar branches, no idle loads
+            v[j] = j < n ? base[j * slot_stride + e] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int j = 0; j < kPrefillMaxUnitsDev; ++j) acc += w[j][c] * v[j];

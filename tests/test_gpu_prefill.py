@@ -93,3 +93,27 @@ def test_prefill_long_contexts_and_unit_lengths(ctx, d, window, pos0, N):
     for i in rows:
         b, e = I.attended_range(pos0 + i, window)
         assert I.rel_err(got[i], orc.attend(q[pos0 + i], K[b:e], V[b:e], 8, 1)) <= TOL, i
+
+
+@pytest.mark.parametrize("pos0,N,window,d", [(0, 4096, 0, 512), (16384, 256, 0, 512), (0, 1024, 0, 512),
+                                             (0, 300, 0, 512), (5000, 333, 512, 256)])
+def test_prefill_schedule_forms(ctx, pos0, N, window, d):
+    """The host schedule takes several forms (a 4096-token causal prompt pairs
+    whole blocks, a deep 256-token chunk cuts every block into 8 units, 1024
+    and 300 tokens are packed stream-K with many split blocks); the rows of
+    the blocks cut into the most units -- merged from the most partials --
+    and of some whole blocks are checked against the oracle."""
+    import g4hip
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    units, _ = g4hip.prefill_schedule(pos0, N, window, d, 1, cus)
+    n_units = np.bincount(units[:, 0], minlength=(N + 7) // 8)
+    order = np.argsort(-n_units, kind="stable")
+    blocks = list(order[:3]) + [b for b in order[::-1] if n_units[b] == 1][:1]
+    print(f"[case] prefill schedule pos0={pos0} N={N} W={window} d={d}: units {len(units)}, "
+          f"most per block {n_units.max()}, checked blocks {blocks}", flush=True)
+    q, K, V = case(77 + d + pos0 + N, pos0 + N, d, d == 512)
+    got = prefill(ctx, q[pos0:], K, V, pos0, N, window, d)
+    rows = sorted({i for b in blocks for i in range(8 * b, min(8 * b + 8, N))})
+    for i in rows:
+        b, e = I.attended_range(pos0 + i, window)
+        assert I.rel_err(got[i], orc.attend(q[pos0 + i], K[b:e], V[b:e], 8, 1)) <= TOL, i
