@@ -87,9 +87,54 @@ struct g4_kv_cache {
     int64_t capacity = 0;
     std::vector<int64_t> width;
     std::vector<float *> k, v;
-    std::vector<int64_t> rows;
+    std::vector<int64_t> rows;  // positions appended
+    // Ring layers keep only their last ring[l] rows: position p at slots
+    // p % R and p % R + R of 2R rows, so any R consecutive positions are
+    // contiguous rows.  0: the whole history, position p at row p.
+    std::vector<int64_t> ring;
     int known_layers = 0;  // layers.len() of the reference's Vec<Layer>
 };
+
+namespace {
+
+// Row of position p (resident) in layer l's storage.
+int64_t slot_of(const g4_kv_cache *c, int l, int64_t p) { return c->ring[l] > 0 ? p % c->ring[l] : p; }
+
+// Copies m rows of positions p.. (m <= R) from contiguous device rows src_k /
+// src_v into ring layer l: each position to its slot and its mirror.
+int ring_store(g4_kv_cache *c, int l, const float *src_k, const float *src_v, int64_t p, int64_t m,
+               hipStream_t stream) {
+    const int64_t R = c->ring[l], w = c->width[l], s0 = p % R;
+    const int64_t m1 = std::min(m, R - s0), m2 = m - m1;  // before and after the wrap
+    const size_t rb = (size_t)w * sizeof(float);
+    for (int64_t mirror = 0; mirror <= R; mirror += R) {
+        G4_HIP(hipMemcpyAsync(c->k[l] + (s0 + mirror) * w, src_k, rb * m1, hipMemcpyDeviceToDevice, stream));
+        G4_HIP(hipMemcpyAsync(c->v[l] + (s0 + mirror) * w, src_v, rb * m1, hipMemcpyDeviceToDevice, stream));
+        if (m2 > 0) {
+            G4_HIP(hipMemcpyAsync(c->k[l] + mirror * w, src_k + m1 * w, rb * m2, hipMemcpyDeviceToDevice, stream));
+            G4_HIP(hipMemcpyAsync(c->v[l] + mirror * w, src_v + m1 * w, rb * m2, hipMemcpyDeviceToDevice, stream));
+        }
+    }
+    return G4_OK;
+}
+
+// After n rows were written at slots [s, s + n) of ring layer l (n <= R,
+// so s + n <= 2R), copies each to its other slot, s +- R.
+int ring_mirror(g4_kv_cache *c, int l, int64_t s, int64_t n, hipStream_t stream) {
+    const int64_t R = c->ring[l], w = c->width[l];
+    const size_t rb = (size_t)w * sizeof(float);
+    const int64_t a0 = s, a1 = std::min(s + n, R);   // below R: mirrors at +R
+    const int64_t b0 = std::max(s, R), b1 = s + n;   // from R on: mirrors at -R
+    for (float *base : {c->k[l], c->v[l]}) {
+        if (a1 > a0)
+            G4_HIP(hipMemcpyAsync(base + (a0 + R) * w, base + a0 * w, rb * (a1 - a0), hipMemcpyDeviceToDevice, stream));
+        if (b1 > b0)
+            G4_HIP(hipMemcpyAsync(base + (b0 - R) * w, base + b0 * w, rb * (b1 - b0), hipMemcpyDeviceToDevice, stream));
+    }
+    return G4_OK;
+}
+
+}  // namespace
 
 extern "C" {
 
@@ -232,31 +277,45 @@ int g4_attend_decode_batch(g4_ctx *ctx, int B, const float *q, const float *k_ba
     });
 }
 
+namespace {
+
+// g4_attend_prefill with the K/V rows starting at position kv_origin (the
+// rows a ring or a windowed view hands over); kv_origin 0 is the public form.
+int attend_prefill_rows(g4_ctx *ctx, const float *q, const float *k_cache, const float *v_cache, int64_t row_stride,
+                        int64_t pos0, int64_t N, int64_t window, int64_t kv_origin, int n_heads, int n_kv_heads,
+                        int head_dim, float scale, float *out, g4_stream stream) {
+    if (!ctx) return invalid("g4_attend_prefill: null context");
+    if (N < 0 || pos0 < 0 || window < 0) return invalid("prefill needs N, pos0, window >= 0");
+    if (N == 0) return (int)G4_OK;
+    int rc = check_heads(n_heads, n_kv_heads, head_dim);
+    if (rc != G4_OK) return rc;
+    if (row_stride < (int64_t)n_kv_heads * head_dim) return invalid("row_stride below the row width");
+    g4::PrefillArgs a{};
+    a.q = q;
+    a.k = k_cache;
+    a.v = v_cache;
+    a.row_stride = row_stride;
+    a.pos0 = pos0;
+    a.N = N;
+    a.window = window;
+    a.kv_origin = kv_origin;
+    a.n_heads = n_heads;
+    a.n_kv_heads = n_kv_heads;
+    a.head_dim = head_dim;
+    a.scale = scale;
+    a.out = out;
+    return g4::launch_prefill(ctx, a, as_stream(stream));
+}
+
+}  // namespace
+
 int g4_attend_prefill(g4_ctx *ctx, const float *q, const float *k_cache, const float *v_cache,
                       int64_t row_stride, int64_t pos0, int64_t N, int64_t window, int n_heads,
                       int n_kv_heads, int head_dim, float scale, float *out, g4_stream stream) {
     return guarded([&] {
         g4::clear_error();
-        if (!ctx) return invalid("g4_attend_prefill: null context");
-        if (N < 0 || pos0 < 0 || window < 0) return invalid("prefill needs N, pos0, window >= 0");
-        if (N == 0) return (int)G4_OK;
-        int rc = check_heads(n_heads, n_kv_heads, head_dim);
-        if (rc != G4_OK) return rc;
-        if (row_stride < (int64_t)n_kv_heads * head_dim) return invalid("row_stride below the row width");
-        g4::PrefillArgs a{};
-        a.q = q;
-        a.k = k_cache;
-        a.v = v_cache;
-        a.row_stride = row_stride;
-        a.pos0 = pos0;
-        a.N = N;
-        a.window = window;
-        a.n_heads = n_heads;
-        a.n_kv_heads = n_kv_heads;
-        a.head_dim = head_dim;
-        a.scale = scale;
-        a.out = out;
-        return g4::launch_prefill(ctx, a, as_stream(stream));
+        return attend_prefill_rows(ctx, q, k_cache, v_cache, row_stride, pos0, N, window, 0, n_heads, n_kv_heads,
+                                   head_dim, scale, out, stream);
     });
 }
 
@@ -348,12 +407,14 @@ int g4_rope_neox_rows(g4_ctx *ctx, float *x, int64_t n_tokens, int n_heads, int 
 }
 
 // ------------------------------------------------------------------ KvCache
-int g4_kv_create(g4_ctx *ctx, int n_layers, const int64_t *widths, int64_t capacity,
-                 g4_kv_cache **out) {
+int g4_kv_create_ring(g4_ctx *ctx, int n_layers, const int64_t *widths, int64_t capacity,
+                      const int64_t *ring_rows, g4_kv_cache **out) {
     return guarded([&] {
         g4::clear_error();
         if (!ctx || !out || !widths) return invalid("g4_kv_create: null argument");
         if (n_layers <= 0 || capacity <= 0) return invalid("g4_kv_create: empty cache shape");
+        for (int l = 0; ring_rows && l < n_layers; ++l)
+            if (ring_rows[l] < 0) return invalid("g4_kv_create: negative ring size");
         *out = nullptr;
         G4_HIP(hipSetDevice(ctx->device));
         auto *c = new g4_kv_cache();
@@ -364,9 +425,13 @@ int g4_kv_create(g4_ctx *ctx, int n_layers, const int64_t *widths, int64_t capac
         c->k.assign(n_layers, nullptr);
         c->v.assign(n_layers, nullptr);
         c->rows.assign(n_layers, 0);
+        c->ring.assign(n_layers, 0);
         for (int l = 0; l < n_layers; ++l) {
             if (c->width[l] <= 0) continue;
-            const size_t bytes = (size_t)capacity * c->width[l] * sizeof(float);
+            // A ring as long as the capacity saves nothing: keep the history.
+            if (ring_rows && ring_rows[l] > 0 && ring_rows[l] < capacity) c->ring[l] = ring_rows[l];
+            const int64_t stored = c->ring[l] > 0 ? 2 * c->ring[l] : capacity;
+            const size_t bytes = (size_t)stored * c->width[l] * sizeof(float);
             hipError_t e = hipMalloc(&c->k[l], bytes);
             if (e == hipSuccess) e = hipMalloc(&c->v[l], bytes);
             if (e != hipSuccess) {
@@ -377,6 +442,11 @@ int g4_kv_create(g4_ctx *ctx, int n_layers, const int64_t *widths, int64_t capac
         *out = c;
         return (int)G4_OK;
     });
+}
+
+int g4_kv_create(g4_ctx *ctx, int n_layers, const int64_t *widths, int64_t capacity,
+                 g4_kv_cache **out) {
+    return g4_kv_create_ring(ctx, n_layers, widths, capacity, nullptr, out);
 }
 
 int g4_kv_destroy(g4_kv_cache *c) {
@@ -403,10 +473,19 @@ int g4_kv_append_rows(g4_kv_cache *c, int layer, const float *k, const float *v,
                                  "context length " + std::to_string(c->rows[layer] + n) +
                                      " exceeds configured max " + std::to_string(c->capacity),
                                  (uint64_t)(c->rows[layer] + n), (uint64_t)c->capacity);
-        const size_t row_bytes = (size_t)c->width[layer] * sizeof(float);
-        const size_t off = (size_t)c->rows[layer] * c->width[layer];
-        G4_HIP(hipMemcpyAsync(c->k[layer] + off, k, row_bytes * n, hipMemcpyDeviceToDevice, as_stream(stream)));
-        G4_HIP(hipMemcpyAsync(c->v[layer] + off, v, row_bytes * n, hipMemcpyDeviceToDevice, as_stream(stream)));
+        const int64_t w = c->width[layer];
+        if (c->ring[layer] > 0) {
+            // Only the last R of the n rows stay resident.
+            const int64_t skip = std::max<int64_t>(0, n - c->ring[layer]);
+            const int rc = ring_store(c, layer, k + skip * w, v + skip * w, c->rows[layer] + skip, n - skip,
+                                      as_stream(stream));
+            if (rc != G4_OK) return rc;
+        } else {
+            const size_t row_bytes = (size_t)w * sizeof(float);
+            const size_t off = (size_t)c->rows[layer] * w;
+            G4_HIP(hipMemcpyAsync(c->k[layer] + off, k, row_bytes * n, hipMemcpyDeviceToDevice, as_stream(stream)));
+            G4_HIP(hipMemcpyAsync(c->v[layer] + off, v, row_bytes * n, hipMemcpyDeviceToDevice, as_stream(stream)));
+        }
         c->rows[layer] += n;
         // context_memory.rs:44-47: appending to layer L makes layers 0..=L exist.
         if (layer + 1 > c->known_layers) c->known_layers = layer + 1;
@@ -418,16 +497,15 @@ int g4_kv_append(g4_kv_cache *c, int layer, const float *k, const float *v, g4_s
     return g4_kv_append_rows(c, layer, k, v, 1, stream);
 }
 
-int g4_kv_view(const g4_kv_cache *c, int layer, int64_t len, const float **k, const float **v,
-               int64_t *row_stride) {
-    g4::clear_error();
-    if (!c || !k || !v) return invalid("g4_kv_view: null argument");
-    if (layer < 0 || len < 0) return invalid("g4_kv_view: negative layer or length");
-    // context_memory.rs:53-69
+namespace {
+
+// view(layer, len)'s outcomes (context_memory.rs:53-69): an error, or OK
+// with *absent set when the layer does not exist and len is 0 (an empty view).
+int view_check(const g4_kv_cache *c, int layer, int64_t len, bool *absent) {
+    *absent = false;
     if (layer >= c->known_layers) {
         if (len == 0) {
-            *k = *v = nullptr;
-            if (row_stride) *row_stride = 0;
+            *absent = true;
             return G4_OK;
         }
         return g4::set_error(G4_ERR_MISSING_LAYER, "layer " + std::to_string(layer) + " has no cached K/V",
@@ -439,8 +517,56 @@ int g4_kv_view(const g4_kv_cache *c, int layer, int64_t len, const float **k, co
                              "context length " + std::to_string(len) + " exceeds configured max " +
                                  std::to_string(have),
                              (uint64_t)len, (uint64_t)have);
+    return G4_OK;
+}
+
+}  // namespace
+
+int g4_kv_view(const g4_kv_cache *c, int layer, int64_t len, const float **k, const float **v,
+               int64_t *row_stride) {
+    g4::clear_error();
+    if (!c || !k || !v) return invalid("g4_kv_view: null argument");
+    if (layer < 0 || len < 0) return invalid("g4_kv_view: negative layer or length");
+    bool absent = false;
+    const int rc = view_check(c, layer, len, &absent);
+    if (rc != G4_OK) return rc;
+    if (absent || layer >= c->n_layers) {  // an empty view of a layer that keeps nothing
+        *k = *v = nullptr;
+        if (row_stride) *row_stride = 0;
+        return G4_OK;
+    }
+    // A ring layer's rows are in position order from row 0 only until it wraps.
+    if (c->ring[layer] > 0 && c->rows[layer] > c->ring[layer] && len > 0)
+        return g4::set_error(G4_ERR_COMPUTE, "layer " + std::to_string(layer) + " keeps only its last " +
+                                                 std::to_string(c->ring[layer]) +
+                                                 " rows; view them with g4_kv_view_rows");
     *k = c->k[layer];
     *v = c->v[layer];
+    if (row_stride) *row_stride = c->width[layer];
+    return G4_OK;
+}
+
+int g4_kv_view_rows(const g4_kv_cache *c, int layer, int64_t begin, int64_t end, const float **k, const float **v,
+                    int64_t *row_stride) {
+    g4::clear_error();
+    if (!c || !k || !v) return invalid("g4_kv_view_rows: null argument");
+    if (layer < 0 || begin < 0 || end < begin) return invalid("g4_kv_view_rows: needs 0 <= begin <= end");
+    bool absent = false;
+    const int rc = view_check(c, layer, end, &absent);  // as view(layer, end)
+    if (rc != G4_OK) return rc;
+    if (absent || layer >= c->n_layers) {
+        *k = *v = nullptr;
+        if (row_stride) *row_stride = 0;
+        return G4_OK;
+    }
+    const int64_t R = c->ring[layer];
+    if (R > 0 && begin < end && begin < c->rows[layer] - R)
+        return g4::set_error(G4_ERR_COMPUTE, "positions before " + std::to_string(c->rows[layer] - R) +
+                                                 " have left layer " + std::to_string(layer) + "'s ring of " +
+                                                 std::to_string(R) + " rows");
+    const int64_t off = slot_of(c, layer, begin) * c->width[layer];
+    *k = c->k[layer] + off;
+    *v = c->v[layer] + off;
     if (row_stride) *row_stride = c->width[layer];
     return G4_OK;
 }
@@ -564,20 +690,31 @@ int plan_layer(const g4_hparams *hp, int layer, const float *rope_freqs, LayerPl
 
 // Reserves rows [rows, rows + n) of an owner layer's cache for a fused
 // append; the row count moves only after the launch succeeded.
+// In a ring layer the n rows go to slots [s, s + n) with s = position % R
+// (contiguous: n <= R), and commit_rows copies them to their mirror slots.
 int owner_rows(g4_kv_cache *c, int layer, int64_t row_width, int64_t n, float **k_rows, float **v_rows) {
     if (layer >= c->n_layers || c->width[layer] <= 0) return invalid("g4_kv_append: layer keeps no K/V");
     if (c->width[layer] != row_width)
         return invalid("g4_layer_attention: the layer's cache width differs from n_kv_heads*head_dim");
     if (c->rows[layer] + n > c->capacity) return context_too_long(c->rows[layer] + n, c->capacity);
-    *k_rows = c->k[layer] + c->rows[layer] * row_width;
-    *v_rows = c->v[layer] + c->rows[layer] * row_width;
+    if (c->ring[layer] > 0 && n > c->ring[layer])
+        return g4::set_error(G4_ERR_COMPUTE, std::to_string(n) + " tokens do not fit layer " + std::to_string(layer) +
+                                                 "'s ring of " + std::to_string(c->ring[layer]) + " rows");
+    const int64_t slot = slot_of(c, layer, c->rows[layer]);
+    *k_rows = c->k[layer] + slot * row_width;
+    *v_rows = c->v[layer] + slot * row_width;
     return G4_OK;
 }
 
-void commit_rows(g4_kv_cache *c, int layer, int64_t n) {
+int commit_rows(g4_kv_cache *c, int layer, int64_t n, hipStream_t stream) {
+    if (c->ring[layer] > 0) {
+        const int rc = ring_mirror(c, layer, slot_of(c, layer, c->rows[layer]), n, stream);
+        if (rc != G4_OK) return rc;
+    }
     c->rows[layer] += n;
     // context_memory.rs:44-47: appending to layer L makes layers 0..=L exist.
     if (layer + 1 > c->known_layers) c->known_layers = layer + 1;
+    return G4_OK;
 }
 
 }  // namespace
@@ -619,21 +756,25 @@ int g4_layer_attention(g4_ctx *ctx, g4_kv_cache *cache, const g4_hparams *hp, in
         rc = prepare(ctx, q, owner ? k : nullptr, v, 1, position, hp->n_heads, hp->n_kv_heads, head_dim, q_norm_w,
                      k_norm_w, hp->rms_norm_eps, pl.base, pl.factors, k_rows, v_rows, row_width, as_stream(stream));
         if (rc != G4_OK) return rc;
-        if (owner) commit_rows(cache, layer, 1);
-        // model.rs:407-408
-        const float *keys = nullptr, *values = nullptr;
-        int64_t stride = 0;
-        rc = g4_kv_view(cache, pl.source, position + 1, &keys, &values, &stride);
-        if (rc != G4_OK) return rc;
+        if (owner) {
+            rc = commit_rows(cache, layer, 1, as_stream(stream));
+            if (rc != G4_OK) return rc;
+        }
+        // model.rs:407-408: view(source, position + 1), then the window's
+        // rows of it -- viewed as that range, which a ring layer also holds.
         int64_t begin = 0, end = position + 1;
         if (!pl.global) g4_windowed_len(position + 1, hp->sliding_window, &begin, &end);
+        const float *keys = nullptr, *values = nullptr;
+        int64_t stride = 0;
+        rc = g4_kv_view_rows(cache, pl.source, begin, end, &keys, &values, &stride);
+        if (rc != G4_OK) return rc;
         if (stride != row_width)
             return invalid("g4_layer_attention: source layer's row width differs from this layer's");
         if (source_out) *source_out = pl.source;
         if (begin_out) *begin_out = begin;
         if (end_out) *end_out = end;
         // model.rs:409-410: q and k are RMS-normalised, so the scale is 1.0.
-        return g4_attend_decode(ctx, q, keys, values, stride, begin, end, hp->n_heads,
+        return g4_attend_decode(ctx, q, keys, values, stride, 0, end - begin, hp->n_heads,
                                 hp->n_kv_heads, head_dim, 1.0f, out, stream);
     });
 }
@@ -671,18 +812,23 @@ int g4_layer_prefill(g4_ctx *ctx, g4_kv_cache *cache, const g4_hparams *hp, int 
                      q_norm_w, k_norm_w, hp->rms_norm_eps, pl.base, pl.factors, k_rows, v_rows, row_width,
                      as_stream(stream));
         if (rc != G4_OK) return rc;
-        if (owner) commit_rows(cache, layer, n_tokens);
-        // The last token's view bounds every earlier one's.
+        if (owner) {
+            rc = commit_rows(cache, layer, n_tokens, as_stream(stream));
+            if (rc != G4_OK) return rc;
+        }
+        // The last token's view bounds every earlier one's; the chunk reads
+        // rows from its first query's window start on.
+        const int64_t lo = (!pl.global && pos0 + 1 > hp->sliding_window) ? pos0 + 1 - hp->sliding_window : 0;
         const float *keys = nullptr, *values = nullptr;
         int64_t stride = 0;
-        rc = g4_kv_view(cache, pl.source, pos0 + n_tokens, &keys, &values, &stride);
+        rc = g4_kv_view_rows(cache, pl.source, lo, pos0 + n_tokens, &keys, &values, &stride);
         if (rc != G4_OK) return rc;
         if (stride != row_width)
             return invalid("g4_layer_prefill: source layer's row width differs from this layer's");
         // Query i attends the rows a decode at position pos0 + i would
         // (model.rs:407-410, eng/mod.rs:10-36), scale 1.0.
-        return g4_attend_prefill(ctx, q, keys, values, stride, pos0, n_tokens, pl.global ? 0 : hp->sliding_window,
-                                 hp->n_heads, hp->n_kv_heads, head_dim, 1.0f, out, stream);
+        return attend_prefill_rows(ctx, q, keys, values, stride, pos0, n_tokens, pl.global ? 0 : hp->sliding_window,
+                                   lo, hp->n_heads, hp->n_kv_heads, head_dim, 1.0f, out, stream);
     });
 }
 

@@ -63,6 +63,7 @@ struct DecodeK {
     const int64_t *kv_end;
     int64_t kv_begin0, kv_end0, max_kv_len;
     int64_t pos0, prefill_window;
+    int64_t kv_origin;  // prefill form: the position of row 0 of k/v
     int n_heads, n_kv_heads, group;
     float scale;
     int chunk_shift;  // keys per split = 1 << chunk_shift
@@ -92,7 +93,7 @@ __device__ inline void seq_range(const DecodeK &p, int s, int64_t &row0, int64_t
     if constexpr (MODE == kPrefill) {
         end = p.pos0 + s + 1;
         begin = (p.prefill_window > 0 && end > p.prefill_window) ? end - p.prefill_window : 0;
-        row0 = 0;
+        row0 = -p.kv_origin;  // key positions from kv_origin on are rows 0, 1, ...
     } else if constexpr (MODE == kBatch) {
         row0 = p.seq_row0[s];
         begin = p.kv_begin[s];
@@ -723,8 +724,8 @@ __global__ __launch_bounds__(256) void decode_generic_kernel(DecodeK p, int D) {
     __shared__ float red[256];
     const float *qh = p.q + ((int64_t)s * p.n_heads + head) * D;
     for (int d = tid; d < D; d += 256) qs[d] = qh[d];
-    const float *kb = p.k + row0 * p.row_stride + (int64_t)kvh * D;
-    const float *vb = p.v + row0 * p.row_stride + (int64_t)kvh * D;
+    const float *kb = p.k + (int64_t)kvh * D;  // key t is row row0 + t
+    const float *vb = p.v + (int64_t)kvh * D;
     constexpr int kMaxPer = 4;  // D <= 1024
     float o[kMaxPer] = {0.0f, 0.0f, 0.0f, 0.0f};
     float m = -INFINITY, l = 0.0f;
@@ -734,7 +735,7 @@ __global__ __launch_bounds__(256) void decode_generic_kernel(DecodeK p, int D) {
         const int64_t t = t0 + tid;
         float x = -INFINITY;
         if (t < end) {
-            const float *kr = kb + t * p.row_stride;
+            const float *kr = kb + (row0 + t) * p.row_stride;
             float acc = 0.0f;
             for (int d = 0; d < D; ++d) acc = fmaf(qs[d], kr[d], acc);
             x = acc * p.scale;
@@ -764,7 +765,7 @@ __global__ __launch_bounds__(256) void decode_generic_kernel(DecodeK p, int D) {
             const int d = tid + 256 * e;
             if (d >= D) break;
             float acc = o[e] * alpha;
-            for (int64_t j = 0; j < nt; ++j) acc = fmaf(ps[j], vb[(t0 + j) * p.row_stride + d], acc);
+            for (int64_t j = 0; j < nt; ++j) acc = fmaf(ps[j], vb[(row0 + t0 + j) * p.row_stride + d], acc);
             o[e] = acc;
         }
         __syncthreads();
@@ -922,6 +923,7 @@ int launch_decode(g4_ctx *ctx, const DecodeArgs &a, hipStream_t stream) {
     p.max_kv_len = a.max_kv_len;
     p.pos0 = a.pos0;
     p.prefill_window = a.prefill_window;
+    p.kv_origin = a.kv_origin;
     p.n_heads = a.n_heads;
     p.n_kv_heads = a.n_kv_heads;
     p.group = a.n_heads / a.n_kv_heads;

@@ -72,6 +72,7 @@ struct DecodeArgs {
     // position pos0 + s, with range [(p+1-window)+ or 0, p+1).
     int64_t pos0;
     int64_t prefill_window;  // -1: not prefill; 0: global; >0: sliding window
+    int64_t kv_origin;       // prefill form: the position of row 0 of k/v
     int n_heads, n_kv_heads, head_dim;
     float scale;
     float *out;
@@ -84,6 +85,7 @@ struct PrefillArgs {
     const float *v;
     int64_t row_stride;
     int64_t pos0, N, window;
+    int64_t kv_origin;  // the position of row 0 of k/v (rows before it are never read)
     int n_heads, n_kv_heads, head_dim;
     float scale;
     float *out;

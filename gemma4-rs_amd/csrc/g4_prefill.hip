@@ -77,6 +77,7 @@ struct PrefillK {
     const float *v;
     int64_t row_stride;
     int64_t pos0, N, window;
+    int64_t kv_origin;  // the position of row 0 of k/v
     int n_heads;
     float scale;
     float *out;
@@ -194,11 +195,11 @@ __device__ __forceinline__ void prefill_unit(const PrefillK &p, const PrefillUni
     const int stride = (int)p.row_stride;  // (pos0 + N) rows of it span < 2^31 bytes (checked by the launcher)
     const int64_t block_lo = (win > 0 && P0 + 1 > win) ? P0 + 1 - win : 0;
     const int n_rows = (int)(last_pos + 1 - block_lo);
-    const float *first_row = p.k + block_lo * p.row_stride + (int64_t)kvh * D;
+    const int64_t first = (block_lo - p.kv_origin) * p.row_stride + (int64_t)kvh * D;  // row of key block_lo
     const __amdgpu_buffer_rsrc_t krs =
-        __builtin_amdgcn_make_buffer_rsrc((void *)first_row, 0, (n_rows - 1) * stride * 4 + D * 4, kBufferWord3);
-    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(p.v + block_lo * p.row_stride + (int64_t)kvh * D), 0, (n_rows - 1) * stride * 4 + D * 4, kBufferWord3);
+        __builtin_amdgcn_make_buffer_rsrc((void *)(p.k + first), 0, (n_rows - 1) * stride * 4 + D * 4, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t vrs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)(p.v + first), 0, (n_rows - 1) * stride * 4 + D * 4, kBufferWord3);
     uint32_t koffs[PER_THREAD], voffs[PER_THREAD];
 #pragma unroll
     for (int e = 0; e < PER_THREAD; ++e) {
@@ -828,7 +829,7 @@ int launch_prefill(g4_ctx *ctx, const PrefillArgs &a, hipStream_t stream) {
     // The MFMA kernel addresses a block's rows with 32-bit byte offsets.
     const bool mfma = (a.head_dim == 256 || a.head_dim == 512) && group == kGroup &&
                       a.n_heads % a.n_kv_heads == 0 &&
-                      (a.pos0 + a.N + 16) * a.row_stride * (int64_t)sizeof(float) < (1LL << 31);
+                      (a.pos0 + a.N + 16 - a.kv_origin) * a.row_stride * (int64_t)sizeof(float) < (1LL << 31);
     if (!mfma) {
         // Any other shape: every query as an independent decode over its range.
         DecodeArgs d{};
@@ -839,6 +840,7 @@ int launch_prefill(g4_ctx *ctx, const PrefillArgs &a, hipStream_t stream) {
         d.row_stride = a.row_stride;
         d.pos0 = a.pos0;
         d.prefill_window = a.window;
+        d.kv_origin = a.kv_origin;
         const int64_t last = a.pos0 + a.N;
         d.max_kv_len = (a.window > 0 && a.window < last) ? a.window : last;
         d.n_heads = a.n_heads;
@@ -860,6 +862,7 @@ int launch_prefill(g4_ctx *ctx, const PrefillArgs &a, hipStream_t stream) {
     p.pos0 = a.pos0;
     p.N = a.N;
     p.window = a.window;
+    p.kv_origin = a.kv_origin;
     p.n_heads = a.n_heads;
     p.scale = a.scale;
     p.out = a.out;

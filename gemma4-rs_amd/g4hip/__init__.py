@@ -69,6 +69,10 @@ _SIGS = {
     "g4_kv_append": (c_int, [c_vp, c_int, c_vp, c_vp, c_vp]),
     "g4_kv_append_rows": (c_int, [c_vp, c_int, c_vp, c_vp, c_i64, c_vp]),
     "g4_kv_view": (c_int, [c_vp, c_int, c_i64, ctypes.POINTER(c_vp), ctypes.POINTER(c_vp), ctypes.POINTER(c_i64)]),
+    "g4_kv_view_rows": (c_int, [c_vp, c_int, c_i64, c_i64, ctypes.POINTER(c_vp), ctypes.POINTER(c_vp),
+                                ctypes.POINTER(c_i64)]),
+    "g4_kv_create_ring": (c_int, [c_vp, c_int, ctypes.POINTER(c_i64), c_i64, ctypes.POINTER(c_i64),
+                                  ctypes.POINTER(c_vp)]),
     "g4_kv_len": (c_i64, [c_vp, c_int]),
     "g4_kv_clear": (None, [c_vp]),
     "g4_layer_attention": (c_int, [c_vp, c_vp, c_vp, c_int, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
@@ -337,10 +341,16 @@ class Context:
 class KvCache:
     """Device-resident ContextMemory (crates/llm-eng/src/context_memory.rs:11-86)."""
 
-    def __init__(self, ctx, widths, capacity):
+    def __init__(self, ctx, widths, capacity, ring_rows=None):
+        """ring_rows: per layer, 0 or the number of last positions a
+        sliding-window ring keeps (g4_kv_create_ring)."""
         arr = (c_i64 * len(widths))(*widths)
         h = c_vp()
-        _raise(lib().g4_kv_create(ctx.handle, len(widths), arr, capacity, ctypes.byref(h)))
+        if ring_rows is None:
+            _raise(lib().g4_kv_create(ctx.handle, len(widths), arr, capacity, ctypes.byref(h)))
+        else:
+            rings = (c_i64 * len(widths))(*ring_rows)
+            _raise(lib().g4_kv_create_ring(ctx.handle, len(widths), arr, capacity, rings, ctypes.byref(h)))
         self.handle = h
         self.ctx = ctx
 
@@ -359,6 +369,13 @@ class KvCache:
         """(k_ptr, v_ptr, row_stride) of the first `length` rows of `layer`."""
         k, v, s = c_vp(), c_vp(), c_i64(0)
         _raise(lib().g4_kv_view(self.handle, layer, length, ctypes.byref(k), ctypes.byref(v), ctypes.byref(s)))
+        return k.value, v.value, s.value
+
+    def view_rows(self, layer, begin, end):
+        """(k_ptr, v_ptr, row_stride) of the rows of positions [begin, end)."""
+        k, v, s = c_vp(), c_vp(), c_i64(0)
+        _raise(lib().g4_kv_view_rows(self.handle, layer, begin, end, ctypes.byref(k), ctypes.byref(v),
+                                     ctypes.byref(s)))
         return k.value, v.value, s.value
 
     def __len__(self):

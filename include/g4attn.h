@@ -152,9 +152,27 @@ int g4_kv_append(g4_kv_cache *cache, int layer, const float *k_dev, const float 
 int g4_kv_append_rows(g4_kv_cache *cache, int layer, const float *k_dev, const float *v_dev,
                       int64_t n, g4_stream stream);
 /* view (context_memory.rs:53-69): the first len rows, or MissingLayer /
- * ContextTooLong with the reference's numbers. */
+ * ContextTooLong with the reference's numbers.  On a ring layer (below) that
+ * has wrapped, G4_ERR_COMPUTE: its first rows are gone. */
 int g4_kv_view(const g4_kv_cache *cache, int layer, int64_t len, const float **k_dev,
                const float **v_dev, int64_t *row_stride);
+/* The rows of positions [begin, end) as one run of rows (k_dev = position
+ * begin's row, row_stride floats apart): the outcomes of view(layer, end),
+ * and on a ring layer G4_ERR_COMPUTE when the range starts before the last
+ * ring_rows positions.  The layer drivers view a window this way. */
+int g4_kv_view_rows(const g4_kv_cache *cache, int layer, int64_t begin, int64_t end,
+                    const float **k_dev, const float **v_dev, int64_t *row_stride);
+/* g4_kv_create with sliding-window rings (no counterpart in the reference,
+ * whose sliding owners keep their whole history, context_memory.rs:11-86):
+ * layer l with 0 < ring_rows[l] < capacity keeps only its last ring_rows[l]
+ * positions, in 2 * ring_rows[l] rows of storage (every position is stored
+ * twice, at p % R and p % R + R, so that any R consecutive positions are one
+ * run of rows).  Positions still count up to capacity (ContextTooLong as
+ * before); the layer drivers read a ring layer exactly as a whole-history
+ * one.  A prefill chunk of n tokens on a layer with window W needs
+ * ring_rows >= W + n - 1.  ring_rows_host may be NULL (no rings). */
+int g4_kv_create_ring(g4_ctx *ctx, int n_layers, const int64_t *widths_host, int64_t capacity,
+                      const int64_t *ring_rows_host, g4_kv_cache **cache);
 int64_t g4_kv_len(const g4_kv_cache *cache, int layer);
 void g4_kv_clear(g4_kv_cache *cache); /* context_memory.rs:82-84 */
 
