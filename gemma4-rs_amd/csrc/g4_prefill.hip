@@ -135,15 +135,21 @@ __device__ inline void load_to_lds(__amdgpu_buffer_rsrc_t rsrc, f32x4 *lds, uint
 // SPLIT wavefronts that divide the head dimension (DH = D / SPLIT dims each),
 // so that one wavefront's Q^T and O^T fit the register file.
 //
-// At D = 256 a wavefront holds Q^T and O^T for the whole head (SPLIT = 1):
-// no exchange of partial scores, 64 KB of LDS, and two workgroups per CU.
-// At D = 512 the head does not fit one wavefront's registers (SPLIT = 2).
+// At D = 512 the head does not fit one wavefront's registers (SPLIT = 2),
+// and each SIMD runs the two waves of a row group.  At D = 256 a wavefront
+// holds Q^T and O^T for the whole head (SPLIT = 1); to give each SIMD two
+// waves there as well, a second group of four waves (KSPLIT = 2) takes the
+// odd tiles of the same rows, keeping its own softmax state, and hands it to
+// the first group at the end of the unit.  One workgroup per CU either way.
 template <int D>
 struct PrefillShape {
-    static constexpr int SPLIT = D == 256 ? 1 : 2;  // the merge grid's z extent is WAVES
+    static constexpr int SPLIT = D == 256 ? 1 : 2;
+    static constexpr int KSPLIT = D == 256 ? 2 : 1;  // wave groups taking alternate tiles
     static constexpr int DH = D / SPLIT;
-    static constexpr int WAVES = kWaves * SPLIT;
+    static constexpr int RWAVES = kWaves * SPLIT;    // waves holding the result (the merge grid's z)
+    static constexpr int WAVES = RWAVES * KSPLIT;
     static constexpr int THREADS = 64 * WAVES;
+    static constexpr int TPS = KSPLIT;               // tiles per step, one per wave group
 };
 
 // One unit: the rows of position block u.block against its key tiles
@@ -156,11 +162,14 @@ __device__ __forceinline__ void prefill_unit(const PrefillK &p, const PrefillUni
     constexpr int NV = DH / 64;  // 64-dim V groups per wave
     constexpr int NT = DH / 16;  // O^T tiles per wave
     constexpr int TILE_F4 = 16 * D / 4;
-    constexpr int PER_THREAD = TILE_F4 / S::THREADS;
+    constexpr int PER_THREAD = TILE_F4 / S::THREADS;  // loads per thread per tile, of K and of V
+    constexpr int TPS = S::TPS;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const int rg = wave % kWaves, half = wave / kWaves;  // row group, dim half
+    const int rg = wave % kWaves;                           // row group
+    const int half = S::SPLIT == 2 ? wave / kWaves : 0;     // dim half
+    const int kpar = S::KSPLIT == 2 ? wave / kWaves : 0;    // tile parity
     const int g = lane >> 4, c = lane & 15;
     const int kvh = blockIdx.y;
 
@@ -172,12 +181,12 @@ __device__ __forceinline__ void prefill_unit(const PrefillK &p, const PrefillUni
     const int64_t win = p.window;
     const int d0 = half * DH;  // first dim of this wave
 
-    // Double-buffered K and V tiles and partial S^T of the D halves, each
-    // buffer its own array: the tile being loaded and the tile being read
-    // are then distinct objects, so the compiler need not wait for the
-    // former's loads before reading the latter.  The epilogue reuses the
-    // four tile arrays (64*D floats) to transpose the output rows.
-    __shared__ f32x4 lds_k0[TILE_F4], lds_v0[TILE_F4], lds_k1[TILE_F4], lds_v1[TILE_F4];
+    // Double-buffered K and V tiles (TPS per buffer, tile j at j*TILE_F4) and
+    // partial S^T of the D halves, each buffer its own array: the tiles being
+    // loaded and the tiles being read are then distinct objects, so the
+    // compiler need not wait for the former's loads before reading the
+    // latter.  The epilogue reuses the four tile arrays.
+    __shared__ f32x4 lds_k0[TPS * TILE_F4], lds_v0[TPS * TILE_F4], lds_k1[TPS * TILE_F4], lds_v1[TPS * TILE_F4];
     __shared__ f32x4 lds_s0[S::WAVES][64], lds_s1[S::WAVES][64];
 
     // K/V tiles go straight from memory to LDS (buffer_load ... lds: lane l
@@ -246,16 +255,26 @@ __device__ __forceinline__ void prefill_unit(const PrefillK &p, const PrefillUni
     float m = -INFINITY, l = 0.0f;
     bool bad = false;
 
-    // Tile t is read from (kb, vb) while tile t+1 loads into (kn, vn).
+    // Tiles t .. t+TPS-1 are read from (kb, vb) -- tile t+j at j*TILE_F4, by
+    // the wave group of parity j -- while the next step's tiles load into
+    // (kn, vn).
     auto step = [&](int t, const f32x4 *kb, const f32x4 *vb, f32x4 (*ls)[64], f32x4 *kn, f32x4 *vn) {
-        // Tile t has landed (this wave's loads, then everyone's), and every
-        // wave is done reading (kn, vn): fetch tile t+1 into them.
+        // This step's tiles have landed (this wave's loads, then everyone's),
+        // and every wave is done reading (kn, vn): fetch the next tiles into
+        // them.  Past the unit's end the last tile is fetched again
+        // (unread), keeping every step's loads unconditional.
         __builtin_amdgcn_s_waitcnt(kVmcntZero);
         __syncthreads();
-        // The last step loads its own tile again (unread), keeping every
-        // step's loads unconditional.
-        const int tn = t + 1 < u.t_hi ? t + 1 : t;
-
+        int tn[TPS];
+#pragma unroll
+        for (int j = 0; j < TPS; ++j) tn[j] = t + TPS + j < u.t_hi ? t + TPS + j : u.t_hi - 1;
+        // This wave's tile; a group with no tile left in the unit computes a
+        // stale one with every score masked (its weights are exactly 0).
+        const int tw = t + kpar;
+        const bool live = S::KSPLIT == 1 || tw < u.t_hi;  // one group: a step's tile is always live
+        const f32x4 *kt = kb + kpar * TILE_F4;
+        const f32x4 *vt = vb + kpar * TILE_F4;
+        constexpr int NL = 2 * PER_THREAD * TPS;  // tile-part loads per step
         // Partial S^T over this wave's DH dims: two independent chains.
         f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -263,17 +282,21 @@ __device__ __forceinline__ void prefill_unit(const PrefillK &p, const PrefillUni
             // The next tile's loads go out one or two per 8 MFMAs, so that
             // they issue while the matrix pipe works rather than queue up
             // behind each other at the top of the step.
-            static_assert(2 * PER_THREAD % NU == 0 || NU % (2 * PER_THREAD) == 0, "loads spread over the chunks");
-            if constexpr (2 * PER_THREAD >= NU) {
+            static_assert(NL % NU == 0 || NU % NL == 0, "loads spread over the chunks");
+            // Load i: tile i / (2 PER_THREAD) of the next step, part i % (2 PER_THREAD).
+            auto load = [&](int i) {
+                const int j = i / (2 * PER_THREAD);
+                issue_part(tn[j], i % (2 * PER_THREAD), kn + j * TILE_F4, vn + j * TILE_F4);
+            };
+            if constexpr (NL >= NU) {
 #pragma unroll
-                for (int i = uu * (2 * PER_THREAD / NU); i < (uu + 1) * (2 * PER_THREAD / NU); ++i)
-                    issue_part(tn, i, kn, vn);
-            } else if (uu % (NU / (2 * PER_THREAD)) == 0) {
-                issue_part(tn, uu / (NU / (2 * PER_THREAD)), kn, vn);
+                for (int i = uu * (NL / NU); i < (uu + 1) * (NL / NU); ++i) load(i);
+            } else if (uu % (NU / NL) == 0) {
+                load(uu / (NU / NL));
             }
             const int ug = d0 / 32 + uu;
-            const f32x4 k0 = kb[((ug * 4 + g) * 2 + 0) * 16 + c];
-            const f32x4 k1 = kb[((ug * 4 + g) * 2 + 1) * 16 + c];
+            const f32x4 k0 = kt[((ug * 4 + g) * 2 + 0) * 16 + c];
+            const f32x4 k1 = kt[((ug * 4 + g) * 2 + 1) * 16 + c];
             f32x4 &acc = (uu & 1) ? acc1 : acc0;
 #pragma unroll
             for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k0[j], qreg[uu][j], acc, 0, 0, 0);
@@ -283,7 +306,7 @@ __device__ __forceinline__ void prefill_unit(const PrefillK &p, const PrefillUni
         // Scheduling: one load per 8 MFMAs of the chunk loop above.
 #pragma unroll
         for (int uu = 0; uu < NU; ++uu) {
-            __builtin_amdgcn_sched_group_barrier(0x010, 2 * PER_THREAD >= NU ? 2 * PER_THREAD / NU : 1, 0);  // VMEM
+            __builtin_amdgcn_sched_group_barrier(0x010, NL >= NU ? NL / NU : 1, 0);  // VMEM
             __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);                                                // MFMA
         }
         f32x4 sc = acc0 + acc1;
@@ -299,9 +322,12 @@ __device__ __forceinline__ void prefill_unit(const PrefillK &p, const PrefillUni
         float sv[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) sv[r] = sc[r] * p.scale;
-        const bool whole = 16LL * t + 15 <= P0 && (win == 0 || 16LL * t > P0 + kPosPerBlock - 1 - win);
-        if (!whole) {
-            const int64_t rel = pos - 16LL * t;  // key - 16t <= rel, and > rel - win
+        const bool whole = 16LL * tw + 15 <= P0 && (win == 0 || 16LL * tw > P0 + kPosPerBlock - 1 - win);
+        if (!live) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sv[r] = -INFINITY;
+        } else if (!whole) {
+            const int64_t rel = pos - 16LL * tw;  // key - 16tw <= rel, and > rel - win
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int kr = 4 * g + r;
@@ -332,48 +358,80 @@ __device__ __forceinline__ void prefill_unit(const PrefillK &p, const PrefillUni
         for (int r = 0; r < 4; ++r)
 #pragma unroll
             for (int U = 0; U < NV; ++U) {
-                const f32x4 vv = vb[(4 * g + r) * (D / 4) + d0 / 4 + 16 * U + c];
+                const f32x4 vv = vt[(4 * g + r) * (D / 4) + d0 / 4 + 16 * U + c];
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
                     o[4 * U + i] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[i], pr[r], o[4 * U + i], 0, 0, 0);
             }
     };
-    issue_tile(u.t_lo, lds_k0, lds_v0);
+#pragma unroll
+    for (int j = 0; j < TPS; ++j)
+        issue_tile(u.t_lo + j < u.t_hi ? u.t_lo + j : u.t_hi - 1, lds_k0 + j * TILE_F4, lds_v0 + j * TILE_F4);
     int t = u.t_lo;
-    for (; t + 1 < u.t_hi; t += 2) {
+    for (; t + TPS < u.t_hi; t += 2 * TPS) {
         step(t, lds_k0, lds_v0, lds_s0, lds_k1, lds_v1);
-        step(t + 1, lds_k1, lds_v1, lds_s1, lds_k0, lds_v0);
+        step(t + TPS, lds_k1, lds_v1, lds_s1, lds_k0, lds_v0);
     }
     if (t < u.t_hi) step(t, lds_k0, lds_v0, lds_s0, lds_k1, lds_v1);
 
     if (__any(bad && row_valid) && lane == 0) atomicOr(p.status, kStatusNonFinite);
-    const float lt = rows_sum(l);
-
     __builtin_amdgcn_s_waitcnt(kVmcntZero);  // the last step's spare loads have landed
+    if constexpr (S::KSPLIT == 2) {
+        // The odd-tile group hands its (m, l, O) to the even-tile group of
+        // the same rows, which combines them as two disjoint key sets.
+        static_assert(kWaves * NT * 64 <= 2 * TPS * TILE_F4, "the hand-over fits two tile arrays");
+        __syncthreads();  // every wave is done with the tile buffers (no tile load is in flight)
+        f32x4 *xo = (rg < 2 ? lds_k0 : lds_v0) + (rg & 1) * (NT * 64);
+        float2 *xm = (float2 *)lds_k1 + rg * 64;
+        if (kpar == 1) {
+#pragma unroll
+            for (int i = 0; i < NT; ++i) xo[i * 64 + lane] = o[i];
+            xm[lane] = float2{m, l};
+        }
+        __syncthreads();
+        if (kpar == 0) {
+            const float2 ml = xm[lane];
+            const float mm = fmaxf(m, ml.x);
+            const float a = (m == -INFINITY) ? 0.0f : exp2_fast((m - mm) * kLog2e);
+            const float b = (ml.x == -INFINITY) ? 0.0f : exp2_fast((ml.x - mm) * kLog2e);
+#pragma unroll
+            for (int i = 0; i < NT; ++i) o[i] = a * o[i] + b * xo[i * 64 + lane];
+            l = a * l + b * ml.y;
+            m = mm;
+        }
+        __syncthreads();  // the hand-over buffers are free again
+    }
+    const float lt = rows_sum(l);
+    const bool result = S::KSPLIT == 1 || wave < S::RWAVES;  // the waves holding the combined rows
     if (u.slot >= 0) {  // partial of a multi-unit block, in the accumulator layout
         const int64_t sl = (int64_t)u.slot * gridDim.y + kvh;
         f32x4 *po = (f32x4 *)(p.part_o + sl * (kWaves * kRowsPerWave * D));
+        if (result) {
 #pragma unroll
-        for (int i = 0; i < NT; ++i) po[(wave * NT + i) * 64 + lane] = o[i];
-        if (g == 0 && half == 0) p.part_ml[sl * (kWaves * kRowsPerWave) + rg * kRowsPerWave + c] = float2{m, lt};
+            for (int i = 0; i < NT; ++i) po[(wave * NT + i) * 64 + lane] = o[i];
+            if (g == 0 && half == 0) p.part_ml[sl * (kWaves * kRowsPerWave) + rg * kRowsPerWave + c] = float2{m, lt};
+        }
         return;
     }
     // Single unit: normalise and write row-major through LDS (coalesced).
     __syncthreads();  // every wave is done with the tile buffers (no tile load is in flight)
-    // WAVES/4 waves' rows per tile array.
-    constexpr int WPA = S::WAVES / 4;
-    static_assert(WPA * kRowsPerWave * DH <= TILE_F4 * 4 && S::WAVES % 4 == 0, "transpose fits the tile buffers");
-    const int ta = wave / WPA;
+    // RWAVES/4 waves' rows per tile array.
+    constexpr int WPA = S::RWAVES / 4;
+    static_assert(WPA * kRowsPerWave * DH <= TPS * TILE_F4 * 4 && S::RWAVES % 4 == 0, "transpose fits the tile buffers");
+    const int ta = (result ? wave : 0) / WPA;
     f32x4 *tb = ta == 0 ? lds_k0 : ta == 1 ? lds_v0 : ta == 2 ? lds_k1 : lds_v1;
     float *tr = (float *)tb + (wave % WPA) * (kRowsPerWave * DH);
     const float inv = 1.0f / lt;
+    if (result) {
 #pragma unroll
-    for (int U = 0; U < NV; ++U)
+        for (int U = 0; U < NV; ++U)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) tr[c * DH + 64 * U + 4 * (4 * g + r) + i] = o[4 * U + i][r] * inv;
+                for (int r = 0; r < 4; ++r) tr[c * DH + 64 * U + 4 * (4 * g + r) + i] = o[4 * U + i][r] * inv;
+    }
     __syncthreads();
+    if (!result) return;
 #pragma unroll
     for (int e = 0; e < kRowsPerWave * DH / 4 / 64; ++e) {
         const int f = lane + 64 * e;
@@ -387,7 +445,7 @@ __device__ __forceinline__ void prefill_unit(const PrefillK &p, const PrefillUni
 
 // A workgroup runs its units in turn (the host's schedule).
 template <int D>
-__global__ __launch_bounds__(PrefillShape<D>::THREADS, PrefillShape<D>::SPLIT == 1 ? 2 : 1) void prefill_kernel(PrefillK p) {
+__global__ __launch_bounds__(PrefillShape<D>::THREADS, 1) void prefill_kernel(PrefillK p) {
     const int first = p.bin_start[blockIdx.x], end = p.bin_start[blockIdx.x + 1];
     for (int i = first; i < end; ++i) {
         // The previous unit's waves are done with the tile buffers (its
@@ -891,11 +949,11 @@ int launch_prefill(g4_ctx *ctx, const PrefillArgs &a, hipStream_t stream) {
         // One merge workgroup per producing wavefront of a block.
         if (D == 256)
             hipLaunchKernelGGL(prefill_merge_kernel<256>,
-                               dim3((unsigned)pl.n_blocks, (unsigned)a.n_kv_heads, (unsigned)PrefillShape<256>::WAVES),
+                               dim3((unsigned)pl.n_blocks, (unsigned)a.n_kv_heads, (unsigned)PrefillShape<256>::RWAVES),
                                dim3(256), 0, stream, p);
         else
             hipLaunchKernelGGL(prefill_merge_kernel<512>,
-                               dim3((unsigned)pl.n_blocks, (unsigned)a.n_kv_heads, (unsigned)PrefillShape<512>::WAVES),
+                               dim3((unsigned)pl.n_blocks, (unsigned)a.n_kv_heads, (unsigned)PrefillShape<512>::RWAVES),
                                dim3(256), 0, stream, p);
         G4_HIP(hipGetLastError());
     }
