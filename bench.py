@@ -394,7 +394,7 @@ def main():
                   "prefill": lambda: bench_prefill(ctx, torch, prep, max(5, k // 10), args.warmup),
                   "ragged": lambda: bench_ragged(ctx, torch, prep, max(5, k // 4), 2),
                   "layer": lambda: bench_layer_steps(ctx, torch, prep, args.steps, args.warmup),
-                  "matvec": lambda: bench_matvec(ctx, torch, max(20, k // 2), 5),
+                  "matvec": lambda: bench_matvec(ctx, torch, max(20, k // 2), args.warmup),
                   "copy": lambda: bench_copy(torch, max(5, k // 4))}[args.only]
             res = fn()
             res.pop("host", None)
@@ -413,7 +413,7 @@ def main():
             workloads["prefill_2048"] = bench_prefill(ctx, torch, prep, max(5, k // 10), args.warmup)
             workloads["ragged_decode_B32"] = bench_ragged(ctx, torch, prep, max(5, k // 4), 2)
             workloads["layer_drivers"] = bench_layer_steps(ctx, torch, prep, args.steps, args.warmup)
-            workloads["q8_0_matvec"] = bench_matvec(ctx, torch, max(20, k // 2), 5)
+            workloads["q8_0_matvec"] = bench_matvec(ctx, torch, max(20, k // 2), args.warmup)
         workloads["global_decode_d512_ctx4096_warm"] = {
             "us_per_layer": g["event_warm"] / args.steps * 1e6,
             "gbs": g["bytes"] / (g["event_warm"] / args.steps) / 1e9,
