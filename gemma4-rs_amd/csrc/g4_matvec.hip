@@ -148,6 +148,26 @@ __global__ __launch_bounds__(64) void matvec_q8_0_kernel(const unsigned char *__
     u32x4 *stage = lds;                                  // [g][NM][chunks]
     float *prod = (float *)(lds + (size_t)g * NM * chunks);  // [NM][rb][pstride]
 
+    const int64_t row0 = (int64_t)blockIdx.x * rb;
+    const int n_rows = (int)min((int64_t)rb, rows - row0);  // >= 1: the grid covers the rows exactly
+    // Stage rows r0 .. r0 + min(g, n_rows - r0) - 1 of each matrix.
+    auto stage_rows = [&](int r0) {
+        const int nr = min(g, n_rows - r0);
+        for (int r = 0; r < nr; ++r)
+#pragma unroll
+            for (int m = 0; m < NM; ++m) {
+                const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                    (void *)((m == 0 ? w : w2) + (row0 + r0 + r) * row_len), 0, row_len, kBufferWord3);
+                u32x4 *dst = stage + (r * NM + m) * chunks;
+                for (int k = 0; k * 64 < chunks; ++k)
+                    if (k * 64 + lane < chunks)
+                        load_to_lds<STREAM ? kNonTemporal : 0>(rs, dst + 64 * k, (uint32_t)(k * 64 + lane) * 16u);
+            }
+    };
+    // The first rows' loads are in flight while the activation is read (and
+    // quantized, when it comes as f32).
+    stage_rows(0);
+
     // This lane's activation blocks: 8 packed int8 dwords and the scale.
     int xqr[NS][8];
     float xsr[NS];
@@ -168,21 +188,9 @@ __global__ __launch_bounds__(64) void matvec_q8_0_kernel(const unsigned char *__
         }
     }
 
-    const int64_t row0 = (int64_t)blockIdx.x * rb;
-    const int n_rows = (int)min((int64_t)rb, rows - row0);
     for (int r0 = 0; r0 < n_rows; r0 += g) {
         const int nr = min(g, n_rows - r0);
-        // Stage rows r0 .. r0 + nr - 1 of each matrix.
-        for (int r = 0; r < nr; ++r)
-#pragma unroll
-            for (int m = 0; m < NM; ++m) {
-                const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-                    (void *)((m == 0 ? w : w2) + (row0 + r0 + r) * row_len), 0, row_len, kBufferWord3);
-                u32x4 *dst = stage + (r * NM + m) * chunks;
-                for (int k = 0; k * 64 < chunks; ++k)
-                    if (k * 64 + lane < chunks)
-                        load_to_lds<STREAM ? kNonTemporal : 0>(rs, dst + 64 * k, (uint32_t)(k * 64 + lane) * 16u);
-            }
+        if (r0 > 0) stage_rows(r0);
         __builtin_amdgcn_s_waitcnt(kVmcntZero);
         __syncthreads();
         for (int r = 0; r < nr; ++r)
