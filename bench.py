@@ -202,11 +202,14 @@ def bench_prefill(ctx, torch, prep, steps, warmup, N=2048):
 
 def bench_layer_steps(ctx, torch, prep, steps, warmup, T=4096, N=2048):
     """The launches of the layer drivers, input preparation included: a
-    global-layer decode step (g4_layer_attention: fused q/k/v norm + RoPE +
-    append of row T-1, then attention over T rows) and a 2048-token prompt
-    through one sliding and one global layer (g4_layer_prefill: the fused
-    preparation of all N tokens with their appends, then the prefill).  The
-    cache rows written are the same each step, so the steps replay as a graph."""
+    global-layer decode step over T rows as g4_layer_attention runs it (one
+    fused launch, g4_decode_step_fused: q norm + RoPE, the new row's k/v norm +
+    RoPE and its append, attention over the T rows, plus the split merge),
+    beside the two-launch form it replaced (g4_prepare_qkv, then
+    g4_attend_decode); and a 2048-token prompt through one sliding and one
+    global layer (g4_layer_prefill: the fused preparation of all N tokens with
+    their appends, then the prefill).  The cache rows written are the same
+    each step, so the steps replay as a graph."""
     res = {}
     d = 512
     freqs = prep.rope_freqs(d)
@@ -216,17 +219,30 @@ def bench_layer_steps(ctx, torch, prep, steps, warmup, T=4096, N=2048):
     wq, wk = torch.ones(d, device="cuda"), torch.ones(d, device="cuda")
     out = torch.zeros(N_HEADS * d, device="cuda")
     row = (T - 1) * N_KV * d
+    k_row, v_row = K.view(-1)[row:], V.view(-1)[row:]
 
-    def step(i):
-        ctx.prepare_qkv(q, k, v, 1, T - 1, N_HEADS, N_KV, d, wq, wk, EPS, GLOBAL_BASE, freqs,
-                        k_rows=K.view(-1)[row:], v_rows=V.view(-1)[row:], row_stride=N_KV * d)
-        ctx.attend_decode(q, K, V, 0, T, N_HEADS, N_KV, d, out)
+    def fused(i):
+        ctx.decode_step_fused(q, k, v, wq, wk, EPS, GLOBAL_BASE, freqs, T - 1, K, V, N_KV * d, T, k_row, v_row,
+                              N_HEADS, N_KV, d, out)
 
-    wall, ev = time_steps(torch, step, steps, warmup, block=20)
+    wall, ev = time_steps(torch, fused, steps, warmup, block=20)
     ctx.check_status()
     res["decode_global_d512_ctx4096_layer_step"] = {"us_per_layer": ev / steps * 1e6,
                                                     "wall_us_per_layer": wall / steps * 1e6,
-                                                    "note": "K/V resident (one copy): preparation + attention"}
+                                                    "note": "K/V resident (one copy): one fused launch + merge"}
+
+    def two_launch(i):
+        # The preparation works in place: repeated steps re-prepare q/k/v
+        # (the norm keeps them bounded), as the step's own launches would.
+        ctx.prepare_qkv(q, k, v, 1, T - 1, N_HEADS, N_KV, d, wq, wk, EPS, GLOBAL_BASE, freqs,
+                        k_rows=k_row, v_rows=v_row, row_stride=N_KV * d)
+        ctx.attend_decode(q, K, V, 0, T, N_HEADS, N_KV, d, out)
+
+    wall, ev = time_steps(torch, two_launch, steps, warmup, block=20)
+    ctx.check_status()
+    res["decode_global_d512_ctx4096_two_launch_step"] = {
+        "us_per_layer": ev / steps * 1e6,
+        "note": "the same step as a preparation launch, then the decode"}
     del K, V
     total_flops, total_s = 0, 0.0
     psteps = max(5, steps // 20)

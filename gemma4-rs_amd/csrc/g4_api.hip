@@ -634,10 +634,11 @@ int context_too_long(int64_t got, int64_t max) {
                          (uint64_t)got, (uint64_t)max);
 }
 
-// Validates and launches the fused preparation (model.rs:394-406).
-int prepare(g4_ctx *ctx, float *q, float *k, float *v, int64_t n_tokens, int64_t pos0, int n_heads,
-            int n_kv_heads, int head_dim, const float *q_w, const float *k_w, float eps, float base,
-            const float *factors, float *k_rows, float *v_rows, int64_t row_stride, hipStream_t stream) {
+// The preparation's argument checks (model.rs:394-406), with the
+// reference's messages for its own failures.
+int prepare_checks(g4_ctx *ctx, const float *q, const float *k, const float *v, int64_t n_tokens, int64_t pos0,
+                   int n_heads, int n_kv_heads, int head_dim, float eps, float base, const float *k_rows,
+                   const float *v_rows, int64_t row_stride) {
     if (!ctx || !q) return invalid("g4_prepare_qkv: null argument");
     if (n_tokens < 0 || pos0 < 0) return invalid("g4_prepare_qkv: negative token count or position");
     if (n_heads <= 0 || head_dim <= 0 || (k && (n_kv_heads <= 0 || !v)))
@@ -648,6 +649,19 @@ int prepare(g4_ctx *ctx, float *q, float *k, float *v, int64_t n_tokens, int64_t
     if (eps < 0.0f) return g4::set_error(G4_ERR_COMPUTE, "invalid RMS norm inputs");
     // ops.rs:142-149 with n_rot = head_dim (rope_heads, model.rs:301)
     if (head_dim % 2 != 0 || base <= 0.0f) return g4::set_error(G4_ERR_COMPUTE, "invalid RoPE inputs");
+    return G4_OK;
+}
+
+// rope_neox's theta_scale, base.powf(-2.0 / n_rot), on the host's libm (ops.rs:151).
+float theta_scale_of(float base, int head_dim) { return powf(base, -2.0f / (float)head_dim); }
+
+// Validates and launches the fused preparation (model.rs:394-406).
+int prepare(g4_ctx *ctx, float *q, float *k, float *v, int64_t n_tokens, int64_t pos0, int n_heads,
+            int n_kv_heads, int head_dim, const float *q_w, const float *k_w, float eps, float base,
+            const float *factors, float *k_rows, float *v_rows, int64_t row_stride, hipStream_t stream) {
+    const int rc = prepare_checks(ctx, q, k, v, n_tokens, pos0, n_heads, n_kv_heads, head_dim, eps, base, k_rows,
+                                  v_rows, row_stride);
+    if (rc != G4_OK) return rc;
     g4::PrepareArgs a{};
     a.q = q;
     a.k = k;
@@ -664,8 +678,7 @@ int prepare(g4_ctx *ctx, float *q, float *k, float *v, int64_t n_tokens, int64_t
     a.n_kv_heads = n_kv_heads;
     a.head_dim = head_dim;
     a.eps = eps;
-    // rope_neox computes base.powf(-2.0 / n_rot) on the host's libm (ops.rs:151).
-    a.theta_scale = powf(base, -2.0f / (float)head_dim);
+    a.theta_scale = theta_scale_of(base, head_dim);
     return g4::launch_prepare_qkv(a, stream);
 }
 
@@ -706,14 +719,23 @@ int owner_rows(g4_kv_cache *c, int layer, int64_t row_width, int64_t n, float **
     return G4_OK;
 }
 
-int commit_rows(g4_kv_cache *c, int layer, int64_t n, hipStream_t stream) {
-    if (c->ring[layer] > 0) {
-        const int rc = ring_mirror(c, layer, slot_of(c, layer, c->rows[layer]), n, stream);
-        if (rc != G4_OK) return rc;
-    }
+// The row count after an append of n rows.
+void count_rows(g4_kv_cache *c, int layer, int64_t n) {
     c->rows[layer] += n;
     // context_memory.rs:44-47: appending to layer L makes layers 0..=L exist.
     if (layer + 1 > c->known_layers) c->known_layers = layer + 1;
+}
+
+// In a ring layer, the mirror copies of positions [p, p + n), written at
+// their primary slots (after the launch that wrote them, on its stream).
+int mirror_rows(g4_kv_cache *c, int layer, int64_t p, int64_t n, hipStream_t stream) {
+    return c->ring[layer] > 0 ? ring_mirror(c, layer, slot_of(c, layer, p), n, stream) : (int)G4_OK;
+}
+
+int commit_rows(g4_kv_cache *c, int layer, int64_t n, hipStream_t stream) {
+    const int rc = mirror_rows(c, layer, c->rows[layer], n, stream);
+    if (rc != G4_OK) return rc;
+    count_rows(c, layer, n);
     return G4_OK;
 }
 
@@ -731,6 +753,73 @@ int g4_prepare_qkv(g4_ctx *ctx, float *q, float *k, float *v, int64_t n_tokens, 
 }
 
 // --------------------------------------------------------- layer attention
+namespace {
+
+// The fused decode step over rows [0, n_rows) of (keys, values), whose last
+// row is `position`; with k, that row is prepared and written to
+// (k_row, v_row) rather than read.  Unsupported shapes: G4_ERR_COMPUTE.
+int decode_step_fused(g4_ctx *ctx, const float *q, const float *k, const float *v, const float *q_w, const float *k_w,
+                      float eps, float base, const float *factors, int64_t position, const float *keys,
+                      const float *values, int64_t row_stride, int64_t n_rows, float *k_row, float *v_row,
+                      int n_heads, int n_kv_heads, int head_dim, float scale, float *out, hipStream_t stream) {
+    int rc = prepare_checks(ctx, q, k, v, 1, position, n_heads, n_kv_heads, head_dim, eps, base, k_row, v_row,
+                            row_stride);
+    if (rc != G4_OK) return rc;
+    if (k && (!k_row || !v_row)) return invalid("fused decode step: the new row needs its cache row");
+    if (!keys || !values || !out) return invalid("fused decode step: null argument");
+    if (n_rows <= 0 || n_rows > position + 1) return invalid("fused decode step: needs 0 < n_rows <= position + 1");
+    g4::DecodeArgs da{};
+    da.B = 1;
+    da.k = keys;
+    da.v = values;
+    da.row_stride = row_stride;
+    da.kv_begin0 = 0;
+    da.kv_end0 = n_rows;
+    da.max_kv_len = n_rows;
+    da.prefill_window = -1;
+    da.n_heads = n_heads;
+    da.n_kv_heads = n_kv_heads;
+    da.head_dim = head_dim;
+    da.scale = scale;
+    da.out = out;
+    if (!g4::layer_decode_fusable(da))
+        return g4::set_error(G4_ERR_COMPUTE, "fused decode step: needs head_dim 256 or 512 and 8 query heads per KV head");
+    g4::LayerPrepArgs lp{};
+    lp.q = q;
+    lp.k = k;
+    lp.v = k ? v : nullptr;
+    lp.q_w = q_w;
+    lp.k_w = k_w;
+    lp.factors = factors;
+    lp.eps = eps;
+    lp.position = position;
+    // rope_neox's angle recurrence (ops.rs:151-160), as the preparation kernels run it.
+    const float theta_scale = theta_scale_of(base, head_dim);
+    float th = (float)position;
+    for (int i = 0; i < head_dim / 2; ++i) {
+        lp.angles[i] = th;
+        th = th * theta_scale;
+    }
+    lp.k_row = k_row;
+    lp.v_row = v_row;
+    return g4::launch_layer_decode(ctx, da, lp, stream);
+}
+
+}  // namespace
+
+int g4_decode_step_fused(g4_ctx *ctx, const float *q, const float *k, const float *v, const float *q_norm_w,
+                         const float *k_norm_w, float eps, float rope_base, const float *freq_factors,
+                         int64_t position, const float *k_cache, const float *v_cache, int64_t row_stride,
+                         int64_t n_rows, float *k_row, float *v_row, int n_heads, int n_kv_heads, int head_dim,
+                         float scale, float *out, g4_stream stream) {
+    return guarded([&] {
+        g4::clear_error();
+        return decode_step_fused(ctx, q, k, v, q_norm_w, k_norm_w, eps, rope_base, freq_factors, position, k_cache,
+                                 v_cache, row_stride, n_rows, k_row, v_row, n_heads, n_kv_heads, head_dim, scale, out,
+                                 as_stream(stream));
+    });
+}
+
 int g4_layer_attention(g4_ctx *ctx, g4_kv_cache *cache, const g4_hparams *hp, int layer,
                        int64_t position, float *q, float *k, float *v, const float *q_norm_w,
                        const float *k_norm_w, const float *rope_freqs, float *out, int *source_out,
@@ -746,9 +835,49 @@ int g4_layer_attention(g4_ctx *ctx, g4_kv_cache *cache, const g4_hparams *hp, in
         const int head_dim = pl.head_dim;
         const int64_t row_width = (int64_t)hp->n_kv_heads * head_dim;
         const bool owner = pl.source == layer;
-        // model.rs:394-406 in one launch: q norm + RoPE; on owner layers k/v
-        // norm, k RoPE and the append into the next cache row.
+        // model.rs:407-408: view(source, position + 1), then the window's rows.
+        int64_t begin = 0, end = position + 1;
+        if (!pl.global) g4_windowed_len(position + 1, hp->sliding_window, &begin, &end);
+        if (source_out) *source_out = pl.source;
+        if (begin_out) *begin_out = begin;
+        if (end_out) *end_out = end;
+        g4::DecodeArgs da{};  // the fused step's shape, for the eligibility test
+        da.B = 1;
+        da.row_stride = row_width;
+        da.kv_end0 = end - begin;
+        da.prefill_window = -1;
+        da.n_heads = hp->n_heads;
+        da.n_kv_heads = hp->n_kv_heads;
+        da.head_dim = head_dim;
         float *k_rows = nullptr, *v_rows = nullptr;
+        if (g4::layer_decode_fusable(da)) {
+            // One launch (plus the split merge): the decode kernel prepares q
+            // and, on an owner layer, the new row, which it appends and
+            // attends (model.rs:394-410).  q, k and v are left as given.
+            rc = prepare_checks(ctx, q, owner ? k : nullptr, v, 1, position, hp->n_heads, hp->n_kv_heads, head_dim,
+                                hp->rms_norm_eps, pl.base, nullptr, nullptr, row_width);
+            if (rc != G4_OK) return rc;
+            if (owner) {
+                rc = owner_rows(cache, layer, row_width, 1, &k_rows, &v_rows);
+                if (rc != G4_OK) return rc;
+                count_rows(cache, layer, 1);
+            }
+            const float *keys = nullptr, *values = nullptr;
+            int64_t stride = 0;
+            rc = g4_kv_view_rows(cache, pl.source, begin, end, &keys, &values, &stride);
+            if (rc != G4_OK) return rc;
+            if (stride != row_width)
+                return invalid("g4_layer_attention: source layer's row width differs from this layer's");
+            // model.rs:409-410: q and k are RMS-normalised, so the scale is 1.0.
+            rc = decode_step_fused(ctx, q, owner ? k : nullptr, v, q_norm_w, k_norm_w, hp->rms_norm_eps, pl.base,
+                                   pl.factors, position, keys, values, stride, end - begin, k_rows, v_rows,
+                                   hp->n_heads, hp->n_kv_heads, head_dim, 1.0f, out, as_stream(stream));
+            if (rc != G4_OK) return rc;
+            return owner ? mirror_rows(cache, layer, position, 1, as_stream(stream)) : (int)G4_OK;
+        }
+        // Other shapes: model.rs:394-406 in one preparation launch (q norm +
+        // RoPE; on owner layers k/v norm, k RoPE and the append), then the
+        // decode over the view.
         if (owner) {
             rc = owner_rows(cache, layer, row_width, 1, &k_rows, &v_rows);
             if (rc != G4_OK) return rc;
@@ -760,20 +889,12 @@ int g4_layer_attention(g4_ctx *ctx, g4_kv_cache *cache, const g4_hparams *hp, in
             rc = commit_rows(cache, layer, 1, as_stream(stream));
             if (rc != G4_OK) return rc;
         }
-        // model.rs:407-408: view(source, position + 1), then the window's
-        // rows of it -- viewed as that range, which a ring layer also holds.
-        int64_t begin = 0, end = position + 1;
-        if (!pl.global) g4_windowed_len(position + 1, hp->sliding_window, &begin, &end);
         const float *keys = nullptr, *values = nullptr;
         int64_t stride = 0;
         rc = g4_kv_view_rows(cache, pl.source, begin, end, &keys, &values, &stride);
         if (rc != G4_OK) return rc;
         if (stride != row_width)
             return invalid("g4_layer_attention: source layer's row width differs from this layer's");
-        if (source_out) *source_out = pl.source;
-        if (begin_out) *begin_out = begin;
-        if (end_out) *end_out = end;
-        // model.rs:409-410: q and k are RMS-normalised, so the scale is 1.0.
         return g4_attend_decode(ctx, q, keys, values, stride, 0, end - begin, hp->n_heads,
                                 hp->n_kv_heads, head_dim, 1.0f, out, stream);
     });

@@ -33,6 +33,7 @@
 // makes the call fail ("softmax input is not finite", model.rs:362-364).
 
 #include "g4_internal.h"
+#include "g4_prep.h"
 
 namespace g4 {
 namespace {
@@ -398,6 +399,28 @@ struct DecodeAcc {
                     o[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(P[t].v[r][i], pr[4 * t + r], o[i], 0, 0, 0);
     }
 
+    // One more key whose value row is held in LDS (vrow, D floats): sv is its
+    // scaled score for head c (-inf for padding columns).
+    __device__ __forceinline__ void fold_key(const L &ln, float sv, const float *vrow) {
+        bad |= __builtin_amdgcn_classf(sv, 0x203);  // signalling/quiet NaN, +inf
+        const bool grow = sv > m + kRescaleSlack;
+        if (__any(grow)) {
+            const float m_new = grow ? sv : m;
+            const float alpha = grow ? exp2_fast((m - m_new) * kLog2e) : 1.0f;
+            l *= alpha;
+#pragma unroll
+            for (int i = 0; i < TW; ++i) o[i] *= alpha;
+            m = m_new;
+        }
+        const float pr = (sv == -INFINITY) ? 0.0f : exp2_fast((sv - m) * kLog2e);
+        if (ln.g == 0) l += pr;  // l is summed over the four lane groups of a head
+        // O^T tile i, component r of lane (g, c): dim base + TW*(4g + r) + i.
+#pragma unroll
+        for (int i = 0; i < TW; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[i][r] += pr * vrow[ln.base + TW * (4 * ln.g + r) + i];
+    }
+
     // The attention output of head c (l summed over the lanes c, c+16, c+32,
     // c+48); out_row = the head's D floats.  A head whose scores were all
     // -inf fails the call.
@@ -443,39 +466,61 @@ struct DecodeAcc {
 // slots, one pair in flight while one is computed; loads are issued
 // unconditionally (clamped to the last pair), so the compiler's wait counts
 // stay exact and never wait on a prefetch.  A pair's second tile past the
-// end (odd tile count) reads zeros and is masked.
+// end (odd tile count) reads zeros and is masked.  prime() issues the first
+// pairs' loads and finish() computes every pair, so that a caller can do
+// other work while the first tiles are in flight.  (A split of at most 16
+// keys is a single tile, which callers load and compute themselves.)
+template <int D, int NBUF, int AUX>
+struct PairPipe {
+    static constexpr int NPAIR = NBUF / 2;
+    KvTile<D> T[NPAIR][2];
+
+    __device__ __forceinline__ void load_pair(const DecodeLane<D> &ln, __amdgpu_buffer_rsrc_t krs,
+                                              __amdgpu_buffer_rsrc_t vrs, int q_first, int n_pairs, int i,
+                                              KvTile<D> (&P)[2]) const {
+        const int q = q_first + (i < n_pairs ? i : n_pairs - 1);
+        ln.template load_tile<AUX>(krs, vrs, 2 * q, P[0]);
+        ln.template load_tile<AUX>(krs, vrs, 2 * q + 1, P[1]);
+    }
+
+    __device__ __forceinline__ void prime(const DecodeLane<D> &ln, __amdgpu_buffer_rsrc_t krs,
+                                          __amdgpu_buffer_rsrc_t vrs, int q_first, int n_pairs) {
+#pragma unroll
+        for (int b = 0; b < NPAIR - 1; ++b) load_pair(ln, krs, vrs, q_first, n_pairs, b, T[b]);
+    }
+
+    __device__ __forceinline__ void finish(const DecodeLane<D> &ln, DecodeAcc<D> &acc, __amdgpu_buffer_rsrc_t krs,
+                                           __amdgpu_buffer_rsrc_t vrs, int q_first, int n_pairs, int n_keys,
+                                           float scale, PairScores<D> &sx, int &buf) {
+        // Steady state: each step issues the loads of the pair NPAIR-1 ahead,
+        // then computes the oldest buffered pair.
+        int i0 = 0;
+        for (; i0 + NPAIR - 1 < n_pairs; i0 += NPAIR) {
+#pragma unroll
+            for (int b = 0; b < NPAIR; ++b) {
+                load_pair(ln, krs, vrs, q_first, n_pairs, i0 + b + NPAIR - 1, T[(b + NPAIR - 1) % NPAIR]);
+                acc.pair(ln, T[b], n_keys - 32 * (q_first + i0 + b), scale, sx, buf);
+            }
+        }
+        // Tail: the remaining (< NPAIR) pairs are already buffered in T[0..].
+#pragma unroll
+        for (int b = 0; b < NPAIR - 1; ++b)
+            if (i0 + b < n_pairs) acc.pair(ln, T[b], n_keys - 32 * (q_first + i0 + b), scale, sx, buf);
+    }
+};
+
 template <int D, int NBUF, int AUX>
 __device__ __forceinline__ void run_pairs(const DecodeLane<D> &ln, DecodeAcc<D> &acc, __amdgpu_buffer_rsrc_t krs,
                                           __amdgpu_buffer_rsrc_t vrs, int q_first, int n_pairs, int n_keys,
                                           float scale, PairScores<D> &sx, int &buf) {
-    constexpr int NPAIR = NBUF / 2;
-    KvTile<D> T[NPAIR][2];
+    PairPipe<D, NBUF, AUX> pp;
     if (n_keys - 32 * q_first <= 16) {  // a single tile: its second half is not computed
-        ln.template load_tile<AUX>(krs, vrs, 2 * q_first, T[0][0]);
-        acc.template pair<1>(ln, T[0], n_keys - 32 * q_first, scale, sx, buf);
+        ln.template load_tile<AUX>(krs, vrs, 2 * q_first, pp.T[0][0]);
+        acc.template pair<1>(ln, pp.T[0], n_keys - 32 * q_first, scale, sx, buf);
         return;
     }
-    auto load_pair = [&](int i, KvTile<D> (&P)[2]) {
-        const int q = q_first + (i < n_pairs ? i : n_pairs - 1);
-        ln.template load_tile<AUX>(krs, vrs, 2 * q, P[0]);
-        ln.template load_tile<AUX>(krs, vrs, 2 * q + 1, P[1]);
-    };
-#pragma unroll
-    for (int b = 0; b < NPAIR - 1; ++b) load_pair(b, T[b]);
-    // Steady state: each step issues the loads of the pair NPAIR-1 ahead,
-    // then computes the oldest buffered pair.
-    int i0 = 0;
-    for (; i0 + NPAIR - 1 < n_pairs; i0 += NPAIR) {
-#pragma unroll
-        for (int b = 0; b < NPAIR; ++b) {
-            load_pair(i0 + b + NPAIR - 1, T[(b + NPAIR - 1) % NPAIR]);
-            acc.pair(ln, T[b], n_keys - 32 * (q_first + i0 + b), scale, sx, buf);
-        }
-    }
-    // Tail: the remaining (< NPAIR) pairs are already buffered in T[0..].
-#pragma unroll
-    for (int b = 0; b < NPAIR - 1; ++b)
-        if (i0 + b < n_pairs) acc.pair(ln, T[b], n_keys - 32 * (q_first + i0 + b), scale, sx, buf);
+    pp.prime(ln, krs, vrs, q_first, n_pairs);
+    pp.finish(ln, acc, krs, vrs, q_first, n_pairs, n_keys, scale, sx, buf);
 }
 
 // One workgroup = one (split, KV head, sequence); NW wavefronts, each owning
@@ -522,6 +567,102 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::NW) void decode_split_kernel(D
         return;
     }
     const int64_t slot = ((int64_t)s * p.n_kv_heads + kvh) * p.max_splits + split;
+    acc.write_partial(ln, p.part_o, p.part_ml, slot, p.group, col_valid);
+}
+
+// The layer driver's decode step with the input preparation fused in (see
+// LayerPrepArgs): one sequence, one workgroup per split as
+// decode_split_kernel, one query head per wavefront of the group.  A
+// workgroup issues its first K/V loads, then, while they are in flight,
+// prepares the group's q heads (and, in the last split of an owner layer,
+// the new row's k and v, which it appends to the cache) with the arithmetic
+// of the standalone preparation kernel; the new row, not in the cache when
+// the loads were issued, is attended from LDS as the range's last key.
+template <int D, int NBUF, int AUX>
+__global__ __launch_bounds__(64 * DecodeShape<D>::NW) void decode_layer_kernel(DecodeK p, LayerPrepArgs lp) {
+    constexpr int NW = DecodeShape<D>::NW;
+    const int split = blockIdx.x, kvh = blockIdx.y;
+    const DecodeLane<D> ln((int)p.row_stride);
+    const int64_t begin = p.kv_begin0, end = p.kv_end0;
+    const int64_t n_splits = p.max_splits;
+    const bool last = split + 1 == n_splits;
+    const bool fresh = lp.k != nullptr && last;  // this workgroup prepares and attends the new row
+    const int64_t k_lo = begin + ((int64_t)split << p.chunk_shift);
+    const int64_t k_hi = last ? end : k_lo + (1LL << p.chunk_shift);
+    const int n_keys = (int)(k_hi - k_lo) - (fresh ? 1 : 0);  // keys read from the cache
+    const int n_pairs = (n_keys + 31) >> 5;
+    const bool single = n_keys <= 16;
+
+    const int stride = (int)p.row_stride;
+    const int64_t first = k_lo * p.row_stride + (int64_t)kvh * D;
+    const int rows = n_keys > 0 ? n_keys : 1;  // with no key to read the resources go unused
+    const __amdgpu_buffer_rsrc_t krs = ln.rows(p.k + first, rows, stride);
+    const __amdgpu_buffer_rsrc_t vrs = ln.rows(p.v + first, rows, stride);
+    PairPipe<D, NBUF, AUX> pp;
+    if (n_keys > 0) {
+        if (single)
+            ln.template load_tile<AUX>(krs, vrs, 0, pp.T[0][0]);
+        else
+            pp.prime(ln, krs, vrs, 0, n_pairs);
+    }
+
+    // The preparation, while those loads are in flight: wavefront w takes
+    // query head kvh*NW + w; in the fresh workgroup waves 0 and 1 then take
+    // the new row's k and v.
+    static_assert(D / 2 <= kPrepMaxAngles, "the angle table covers the head");
+    __shared__ float qp[NW][D];
+    __shared__ float kvn[2][D];
+    __shared__ float sk[NW];
+    {
+        PrepRow<D> row;
+        prep_load<D>(row, ln.lane, lp.q + ((int64_t)kvh * NW + ln.wave) * D, lp.q_w, lp.factors, true);
+        prep_load_angles<D>(row, ln.lane, lp.angles);
+        prep_compute<D>(row, lp.q_w != nullptr, true, lp.eps);
+        prep_store<D>(row, ln.lane, qp[ln.wave]);
+        if (fresh && ln.wave < 2) {
+            const bool is_k = ln.wave == 0;
+            PrepRow<D> kv;
+            prep_load<D>(kv, ln.lane, (is_k ? lp.k : lp.v) + (int64_t)kvh * D, is_k ? lp.k_w : nullptr, lp.factors,
+                         is_k);
+            if (is_k) prep_load_angles<D>(kv, ln.lane, lp.angles);
+            prep_compute<D>(kv, is_k && lp.k_w != nullptr, is_k, lp.eps);
+            prep_store<D>(kv, ln.lane, kvn[ln.wave]);
+            prep_store<D>(kv, ln.lane, (is_k ? lp.k_row : lp.v_row) + (int64_t)kvh * D);  // the append
+        }
+        __syncthreads();
+    }
+
+    const bool col_valid = ln.c < p.group;
+    const int hc = col_valid ? ln.c : 0;
+    DecodeAcc<D> acc;
+    acc.bad = false;
+    acc.start(ln, qp[hc], col_valid);
+    __shared__ PairScores<D> sx;
+    int buf = 0;
+    if (n_keys > 0) {
+        if (single)
+            acc.template pair<1>(ln, pp.T[0], n_keys, p.scale, sx, buf);
+        else
+            pp.finish(ln, acc, krs, vrs, 0, n_pairs, n_keys, p.scale, sx, buf);
+    }
+    if (fresh) {
+        // The new row's score: one head's dot product per wavefront.
+        float dot = 0.0f;
+#pragma unroll
+        for (int m = 0; m < D / 64; ++m) dot += qp[ln.wave][ln.lane + 64 * m] * kvn[0][ln.lane + 64 * m];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) dot += __shfl_xor(dot, off);
+        if (ln.lane == 0) sk[ln.wave] = dot;
+        __syncthreads();
+        acc.fold_key(ln, col_valid ? sk[hc] * p.scale : -INFINITY, kvn[1]);
+    }
+
+    if (ln.wave == 0 && __any(acc.bad && col_valid) && ln.lane == 0) atomicOr(p.status, kStatusNonFinite);
+    if (n_splits == 1) {
+        acc.write_output(ln, p.out + ((int64_t)kvh * p.group + hc) * D, col_valid, p.status);
+        return;
+    }
+    const int64_t slot = (int64_t)kvh * p.max_splits + split;
     acc.write_partial(ln, p.part_o, p.part_ml, slot, p.group, col_valid);
 }
 
@@ -814,8 +955,11 @@ int launch_stream(g4_ctx *ctx, const DecodeArgs &a, DecodeK p, hipStream_t strea
     return G4_OK;
 }
 
+// lp: the fused layer step (one sequence), launched as decode_layer_kernel
+// with the split kernel's sizing.
 template <int MODE>
-int launch_mode(g4_ctx *ctx, const DecodeArgs &a, DecodeK p, hipStream_t stream) {
+int launch_mode(g4_ctx *ctx, const DecodeArgs &a, DecodeK p, hipStream_t stream,
+                const LayerPrepArgs *lp = nullptr) {
     const int D = a.head_dim;
     const int group = p.group;
     const bool mfma = (D == 256 || D == 512) && group <= 16 && a.n_heads % a.n_kv_heads == 0 &&
@@ -879,7 +1023,23 @@ int launch_mode(g4_ctx *ctx, const DecodeArgs &a, DecodeK p, hipStream_t stream)
     }
     dim3 grid((unsigned)max_splits, (unsigned)a.n_kv_heads, (unsigned)a.B);
     const bool stream_kv = MODE == kSingle && max_splits > 1;  // K/V read once per step: NT loads
-    if (D == 256) {
+    if (MODE == kSingle && lp) {
+        if (D == 256) {
+            if (stream_kv)
+                hipLaunchKernelGGL((decode_layer_kernel<256, kDecodeBuffers, kNonTemporal>), grid,
+                                   dim3(64 * DecodeShape<256>::NW), 0, stream, p, *lp);
+            else
+                hipLaunchKernelGGL((decode_layer_kernel<256, kDecodeBuffers, 0>), grid,
+                                   dim3(64 * DecodeShape<256>::NW), 0, stream, p, *lp);
+        } else {
+            if (stream_kv)
+                hipLaunchKernelGGL((decode_layer_kernel<512, kDecodeBuffers, kNonTemporal>), grid,
+                                   dim3(64 * DecodeShape<512>::NW), 0, stream, p, *lp);
+            else
+                hipLaunchKernelGGL((decode_layer_kernel<512, kDecodeBuffers, 0>), grid,
+                                   dim3(64 * DecodeShape<512>::NW), 0, stream, p, *lp);
+        }
+    } else if (D == 256) {
         if (stream_kv)
             hipLaunchKernelGGL((decode_split_kernel<256, MODE, kDecodeBuffers, kNonTemporal>), grid,
                                dim3(64 * DecodeShape<256>::NW), 0, stream, p);
@@ -940,6 +1100,32 @@ int launch_decode(g4_ctx *ctx, const DecodeArgs &a, hipStream_t stream) {
         return launch_mode<kBatch>(ctx, a, p, stream);
     }
     return launch_mode<kSingle>(ctx, a, p, stream);
+}
+
+bool layer_decode_fusable(const DecodeArgs &a) {
+    return a.B == 1 && !a.kv_begin && a.prefill_window < 0 && (a.head_dim == 256 || a.head_dim == 512) &&
+           a.n_kv_heads > 0 && a.n_heads == kDecodeWaves * a.n_kv_heads && a.row_stride <= (1LL << 25) &&
+           a.kv_end0 > a.kv_begin0;
+}
+
+int launch_layer_decode(g4_ctx *ctx, const DecodeArgs &a, const LayerPrepArgs &lp, hipStream_t stream) {
+    if (!layer_decode_fusable(a)) return set_error(G4_ERR_COMPUTE, "fused layer decode: unsupported shape");
+    DecodeK p{};
+    p.q = lp.q;
+    p.k = a.k;
+    p.v = a.v;
+    p.row_stride = a.row_stride;
+    p.kv_begin0 = a.kv_begin0;
+    p.kv_end0 = a.kv_end0;
+    p.max_kv_len = a.max_kv_len;
+    p.prefill_window = -1;
+    p.n_heads = a.n_heads;
+    p.n_kv_heads = a.n_kv_heads;
+    p.group = a.n_heads / a.n_kv_heads;
+    p.scale = a.scale;
+    p.out = a.out;
+    p.status = ctx->status_dev;
+    return launch_mode<kSingle>(ctx, a, p, stream, &lp);
 }
 
 }  // namespace g4

@@ -79,6 +79,30 @@ struct DecodeArgs {
 };
 int launch_decode(g4_ctx *ctx, const DecodeArgs &a, hipStream_t stream);
 
+// A layer's decode step with its input preparation fused in (the layer
+// driver's form): the decode kernel prepares q itself (rms_norm with q_w,
+// NEOX RoPE at `position`) and, on owner layers, the new row's k and v,
+// which it appends at k_row/v_row and attends as the range's last key.  q, k
+// and v are read, not modified.  The DecodeArgs are a single range whose
+// last row is `position`; on an owner layer that row is not read from the
+// cache.
+constexpr int kPrepMaxAngles = 256;  // head_dim 512
+struct LayerPrepArgs {
+    const float *q;                  // [n_heads][head_dim]
+    const float *k, *v;              // [n_kv_heads][head_dim]; k == nullptr on a KV-shared layer
+    const float *q_w, *k_w, *factors;
+    float eps;
+    int64_t position;
+    float *k_row, *v_row;            // owner layers: the cache row of `position`
+    // rope_neox's angles at `position`, theta_i = position * theta_scale^i by
+    // the reference's sequential recurrence, computed on the host (f32
+    // multiplication rounds the same there) so that no workgroup spends the
+    // 256 dependent steps; head_dim/2 of them are used.
+    float angles[kPrepMaxAngles];
+};
+bool layer_decode_fusable(const DecodeArgs &a);
+int launch_layer_decode(g4_ctx *ctx, const DecodeArgs &a, const LayerPrepArgs &lp, hipStream_t stream);
+
 struct PrefillArgs {
     const float *q;
     const float *k;

@@ -4,6 +4,7 @@
 #include <algorithm>
 
 #include "g4_internal.h"
+#include "g4_prep.h"
 
 namespace g4 {
 namespace {
@@ -185,7 +186,7 @@ constexpr int kPrepMaxRowsPerGroup = 16;
 template <int D>
 __global__ __launch_bounds__(64 * kPrepMaxRowsPerGroup) void prepare_heads_kernel(PrepareArgs a) {
 #pragma clang fp contract(off)
-    constexpr int E = D / 64, HALF = D / 2, PE = E / 2;  // elements and pairs per lane
+    constexpr int HALF = D / 2;
     __shared__ float theta[HALF];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t t = blockIdx.x;
@@ -211,61 +212,15 @@ __global__ __launch_bounds__(64 * kPrepMaxRowsPerGroup) void prepare_heads_kerne
         rope = false;
         if (a.v_rows) cache = a.v_rows + t * a.row_stride + (int64_t)h * D;
     }
-    float xv[E], wv[E], fv[PE];
-    if (active) {
-#pragma unroll
-        for (int m = 0; m < E; ++m) xv[m] = x[lane + 64 * m];
-        if (w) {
-#pragma unroll
-            for (int m = 0; m < E; ++m) wv[m] = w[lane + 64 * m];
-        }
-        if (rope) {
-#pragma unroll
-            for (int m = 0; m < PE; ++m) fv[m] = a.factors ? a.factors[lane + 64 * m] : 1.0f;
-        }
-    }
-    if (threadIdx.x == 0) {
-        float th = (float)(a.pos0 + t);
-        for (int i = 0; i < HALF; ++i) {
-            theta[i] = th;
-            th = th * a.theta_scale;
-        }
-    }
+    PrepRow<D> row;
+    if (active) prep_load<D>(row, lane, x, w, a.factors, rope);
+    if (threadIdx.x == 0) prep_angles(theta, HALF, a.pos0 + t, a.theta_scale);
     __syncthreads();
     if (!active) return;
-    double sum = 0.0;
-#pragma unroll
-    for (int m = 0; m < E; ++m) {
-        const float sq = xv[m] * xv[m];
-        sum += (double)sq;
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
-    const float mean = (float)(sum / (double)D);
-    const float root = (float)sqrt((double)(mean + a.eps));
-    const float scale = (float)(1.0 / (double)root);
-#pragma unroll
-    for (int m = 0; m < E; ++m) {
-        xv[m] = xv[m] * scale;
-        if (w) xv[m] = xv[m] * wv[m];
-    }
-    if (rope) {
-#pragma unroll
-        for (int m = 0; m < PE; ++m) {
-            const float angle = theta[lane + 64 * m] / fv[m];
-            float sn, cs;
-            sincosf(angle, &sn, &cs);
-            const float p = xv[m], q = xv[m + PE];
-            xv[m] = p * cs - q * sn;
-            xv[m + PE] = p * sn + q * cs;
-        }
-    }
-#pragma unroll
-    for (int m = 0; m < E; ++m) x[lane + 64 * m] = xv[m];
-    if (cache) {
-#pragma unroll
-        for (int m = 0; m < E; ++m) cache[lane + 64 * m] = xv[m];
-    }
+    if (rope) prep_load_angles<D>(row, lane, theta);
+    prep_compute<D>(row, w != nullptr, rope, a.eps);
+    prep_store<D>(row, lane, x);
+    if (cache) prep_store<D>(row, lane, cache);
 }
 
 // matmul_f32 (ops.rs:9-39): row-major [m,k] x [k,n], sequential inner sum of

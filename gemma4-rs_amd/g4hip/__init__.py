@@ -79,6 +79,8 @@ _SIGS = {
                                    ctypes.POINTER(c_int), ctypes.POINTER(c_i64), ctypes.POINTER(c_i64), c_vp]),
     "g4_prepare_qkv": (c_int, [c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_int, c_int, c_int, c_vp, c_vp, c_f32, c_f32,
                                c_vp, c_vp, c_vp, c_i64, c_vp]),
+    "g4_decode_step_fused": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_f32, c_f32, c_vp, c_i64, c_vp, c_vp,
+                                     c_i64, c_i64, c_vp, c_vp, c_int, c_int, c_int, c_f32, c_vp, c_vp]),
     "g4_layer_prefill": (c_int, [c_vp, c_vp, c_vp, c_int, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                                  ctypes.POINTER(c_int), c_vp]),
     "g4_quantize_q8_0": (c_int, [c_vp, c_vp, c_i64, c_vp, c_vp, c_vp]),
@@ -283,6 +285,15 @@ class Context:
         _raise(lib().g4_prepare_qkv(self.handle, _ptr(q), _ptr(k), _ptr(v), n_tokens, pos0, n_heads, n_kv_heads,
                                     head_dim, _ptr(q_norm_w), _ptr(k_norm_w), eps, rope_base, _ptr(freq_factors),
                                     _ptr(k_rows), _ptr(v_rows), row_stride, _stream(stream)))
+
+    def decode_step_fused(self, q, k, v, q_norm_w, k_norm_w, eps, rope_base, freq_factors, position, k_cache,
+                          v_cache, row_stride, n_rows, k_row, v_row, n_heads, n_kv_heads, head_dim, out, scale=1.0,
+                          stream=None):
+        """g4_decode_step_fused: q (and, with k, the new row) prepared inside the decode kernel."""
+        _raise(lib().g4_decode_step_fused(self.handle, _ptr(q), _ptr(k), _ptr(v), _ptr(q_norm_w), _ptr(k_norm_w), eps,
+                                          rope_base, _ptr(freq_factors), position, _ptr(k_cache), _ptr(v_cache),
+                                          row_stride, n_rows, _ptr(k_row), _ptr(v_row), n_heads, n_kv_heads, head_dim,
+                                          scale, _ptr(out), _stream(stream)))
 
     # -- mat-vecs over GGUF weight formats -----------------------------------
     def quantize_q8_0(self, x, n, scales, quants, stream=None):

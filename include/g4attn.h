@@ -189,10 +189,31 @@ typedef struct {
  * projected q/k/v on, on the device: norm_heads(q, attn_q_norm), RoPE(q); for
  * owner layers norm_heads(k, attn_k_norm), norm_heads(v, none), RoPE(k),
  * append; view(kv_source_layer, pos+1); window range; attend(scale 1.0).
- * q_dev [n_heads*head_dim] and k_dev/v_dev [n_kv_heads*head_dim] are
- * normalised/rotated in place (k/v ignored on shared layers).  rope_freqs_dev
- * ([head_dim_global/2]) is used on global layers.  source, kv_begin, kv_end
- * (host, may be NULL) receive the attended set. */
+ * q_dev [n_heads*head_dim] and k_dev/v_dev [n_kv_heads*head_dim] (k/v
+ * ignored on shared layers): with head_dim 256 or 512 and 8 query heads per
+ * KV head the step is g4_decode_step_fused, which prepares them inside the
+ * attention kernel and leaves them as given; other shapes run the
+ * preparation first, in place.  rope_freqs_dev ([head_dim_global/2]) is used
+ * on global layers.  source, kv_begin, kv_end (host, may be NULL) receive
+ * the attended set. */
+/* One decode step of a layer with its input preparation fused into the
+ * attention kernel (no counterpart in the reference, whose steps are
+ * separate, model.rs:394-410): the kernel applies norm_heads(q, q_norm_w) and
+ * RoPE at `position` (rope_base, freq_factors_dev or NULL) to q_dev
+ * [n_heads*head_dim]; with k_dev, also norm_heads(k, k_norm_w) + RoPE and
+ * norm_heads(v, none) to k_dev/v_dev [n_kv_heads*head_dim], writes them to
+ * k_row_dev/v_row_dev (the cache row of `position`) and attends them as the
+ * last of the n_rows rows of k_cache_dev/v_cache_dev, which it does not
+ * read.  Without k_dev (a KV-shared layer) all n_rows rows are read.
+ * q/k/v are not modified; nothing moves on the host, so a captured graph can
+ * replay it.  head_dim 256 or 512 with 8 query heads per KV head, else
+ * G4_ERR_COMPUTE. */
+int g4_decode_step_fused(g4_ctx *ctx, const float *q_dev, const float *k_dev, const float *v_dev,
+                         const float *q_norm_w_dev, const float *k_norm_w_dev, float eps, float rope_base,
+                         const float *freq_factors_dev, int64_t position, const float *k_cache_dev,
+                         const float *v_cache_dev, int64_t row_stride, int64_t n_rows, float *k_row_dev,
+                         float *v_row_dev, int n_heads, int n_kv_heads, int head_dim, float scale,
+                         float *out_dev, g4_stream stream);
 int g4_layer_attention(g4_ctx *ctx, g4_kv_cache *cache, const g4_hparams *hp, int layer,
                        int64_t position, float *q_dev, float *k_dev, float *v_dev,
                        const float *q_norm_w_dev, const float *k_norm_w_dev,

@@ -1,0 +1,100 @@
+"""The fused layer decode step (g4_decode_step_fused, what g4_layer_attention
+runs for head_dim 256/512 and 8 query heads per KV head): the decode kernel
+prepares q -- and on an owner layer the new row's k and v, which it appends
+-- itself (model.rs:394-410).
+
+Against the two-launch form (g4_prepare_qkv, then g4_attend_decode over the
+appended cache): the appended row must be the same bits, q/k/v must be left
+as given, and the output must match the oracle's attend over the prepared
+rows within the reference's tolerance (synthetic_generate.rs:74-83).  The
+cache row the kernel appends is not read by it: it holds NaN beforehand."""
+import numpy as np
+import pytest
+import torch
+
+import inputs as I
+from oracle import pyoracle as orc
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+EPS = 1e-6
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+CASES = [  # d, attended rows, position of the last row, owner layer, KV heads
+    (512, 4096, 4095, True, 1), (512, 1, 0, True, 1), (512, 40, 39, True, 1), (512, 64, 63, True, 1),
+    (512, 65, 64, True, 1), (512, 9000, 8999, True, 1), (256, 512, 1200, True, 1), (256, 17, 16, True, 1),
+    (256, 512, 700, False, 1), (512, 3000, 2999, False, 1), (512, 300, 299, True, 2), (256, 100, 99, False, 2),
+]
+
+
+@pytest.mark.parametrize("d,n,pos,owner,n_kv", CASES)
+def test_fused_step_matches_prepare_then_decode(ctx, d, n, pos, owner, n_kv):
+    print(f"[case] fused step d={d} rows={n} position={pos} owner={owner} kv={n_kv}", flush=True)
+    rng = np.random.default_rng(d + n + pos + n_kv)
+    n_heads = 8 * n_kv
+    glob = d == 512
+    base = I.GLOBAL_BASE if glob else I.LOCAL_BASE
+    freqs = I.rope_freqs(d + 1, d) if glob else None
+    stride = n_kv * d
+    q = (rng.standard_normal(n_heads * d) * 2).astype(np.float32)
+    k = (rng.standard_normal(n_kv * d) * 2).astype(np.float32)
+    v = (rng.standard_normal(n_kv * d) * 2).astype(np.float32)
+    wq = rng.uniform(0.5, 1.5, d).astype(np.float32)
+    wk = rng.uniform(0.5, 1.5, d).astype(np.float32)
+    rows = rng.standard_normal((n, stride)).astype(np.float32)
+    vrows = rng.standard_normal((n, stride)).astype(np.float32)
+
+    # the two-launch form: prepare (appending row n-1 on an owner layer), then decode
+    K1, V1 = dev(rows), dev(vrows)
+    q1, k1, v1 = dev(q), dev(k), dev(v)
+    ctx.prepare_qkv(q1, k1 if owner else None, v1 if owner else None, 1, pos, n_heads, n_kv, d, dev(wq), dev(wk),
+                    EPS, base, dev(freqs) if glob else None,
+                    k_rows=K1.view(-1)[(n - 1) * stride:] if owner else None,
+                    v_rows=V1.view(-1)[(n - 1) * stride:] if owner else None, row_stride=stride)
+    ref_out = torch.zeros(n_heads * d, device="cuda")
+    ctx.attend_decode(q1, K1, V1, 0, n, n_heads, n_kv, d, ref_out)
+
+    # the fused step over a cache whose new row is NaN until the kernel writes it
+    rows2, vrows2 = rows.copy(), vrows.copy()
+    if owner:
+        rows2[n - 1] = np.nan
+        vrows2[n - 1] = np.nan
+    K2, V2 = dev(rows2), dev(vrows2)
+    q2, k2, v2 = dev(q), dev(k), dev(v)
+    out = torch.zeros(n_heads * d, device="cuda")
+    ctx.decode_step_fused(q2, k2 if owner else None, v2, dev(wq), dev(wk), EPS, base, dev(freqs) if glob else None,
+                          pos, K2, V2, stride, n, K2.view(-1)[(n - 1) * stride:] if owner else None,
+                          V2.view(-1)[(n - 1) * stride:] if owner else None, n_heads, n_kv, d, out)
+    ctx.check_status()
+
+    # q/k/v untouched; the appended row is the prepared row, bit for bit
+    assert np.array_equal(host(q2), q) and np.array_equal(host(k2), k) and np.array_equal(host(v2), v)
+    if owner:
+        assert np.array_equal(host(K2)[n - 1], host(K1)[n - 1])
+        assert np.array_equal(host(V2)[n - 1], host(V1)[n - 1])
+    got = host(out)
+    assert I.rel_err(got, host(ref_out)) <= TOL
+    ref = orc.attend(host(q1), host(K1), host(V1), n_heads, n_kv)
+    assert I.rel_err(got, ref) <= TOL
+
+
+def test_fused_step_rejects_other_shapes(ctx):
+    import g4hip
+    d, n = 128, 10
+    z = torch.zeros(8 * d, device="cuda")
+    K = torch.zeros(n * d, device="cuda")
+    with pytest.raises(g4hip.EngError, match="8 query heads per KV head"):
+        ctx.decode_step_fused(z, None, None, None, None, EPS, 10000.0, None, n - 1, K, K, d, n, None, None, 8, 1, d,
+                              torch.zeros(8 * d, device="cuda"))
+    with pytest.raises(g4hip.EngError, match="n_rows"):
+        ctx.decode_step_fused(z, None, None, None, None, EPS, 10000.0, None, 3, K, K, d, n, None, None, 8, 1, 256,
+                              torch.zeros(8 * 256, device="cuda"))

@@ -122,3 +122,24 @@ def test_q8_0_matvecs_in_a_graph(ctx, rows, cols):
         ctx.gated_ffn_q8_0(w, up, rows, cols, x, b)
 
     replay_and_check(ctx, run, [x], [a, b], lambda i: [torch.randn(cols, device="cuda") * (i + 1)])
+
+
+def test_fused_decode_step_in_a_graph(ctx):
+    """A global layer step as g4_layer_attention runs it: one launch that
+    prepares q and the new row, appends the row and attends (plus the merge)."""
+    d, T = 512, 2048
+    rng = np.random.default_rng(9)
+    K = dev(rng.standard_normal((T, d)).astype(np.float32))
+    V = dev(rng.standard_normal((T, d)).astype(np.float32))
+    q, k, v = (dev(rng.standard_normal(n).astype(np.float32)) for n in (8 * d, d, d))
+    wq, wk = dev(rng.uniform(0.5, 1.5, d).astype(np.float32)), dev(rng.uniform(0.5, 1.5, d).astype(np.float32))
+    freqs = dev(I.rope_freqs(4, d))
+    out = torch.zeros(8 * d, device="cuda")
+
+    def run():
+        ctx.decode_step_fused(q, k, v, wq, wk, 1e-6, I.GLOBAL_BASE, freqs, T - 1, K, V, d, T,
+                              K.view(-1)[(T - 1) * d:], V.view(-1)[(T - 1) * d:], 8, 1, d, out)
+
+    replay_and_check(ctx, run, [q, k, v], [out],
+                     lambda i: [torch.randn(8 * d, device="cuda"), torch.randn(d, device="cuda"),
+                                torch.randn(d, device="cuda")])
