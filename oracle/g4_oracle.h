@@ -1,7 +1,7 @@
 /*
  * g4_oracle.h -- CPU restatement of gemma4-rs's attention path.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the checker that the HIP
+ * TEST INFRASTRUCTURE ONLY.  This library is the oracle that the HIP
  * attention backend is compared against.  Only the test suite, the smoke
  * check and the CPU-baseline leg of the benchmark may load it; the product
  * library never links, loads or calls it.

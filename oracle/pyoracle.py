@@ -1,8 +1,8 @@
 """ctypes binding of the oracle (liboracle.so) -- TEST INFRASTRUCTURE ONLY.
 
 The oracle restates gemma4-rs's CPU attention path in C (g4_oracle.c).  It is
-the checker: only the test suite, the smoke check and the CPU-baseline leg of
-the benchmark load it.
+what results are compared against: only the test suite, the smoke check and
+the CPU-baseline leg of the benchmark load it.
 """
 import ctypes
 import os
