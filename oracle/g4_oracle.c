@@ -1,7 +1,7 @@
 /*
  * g4_oracle.c -- CPU restatement of gemma4-rs's attention path.
  *
- * TEST INFRASTRUCTURE ONLY: the checker for the HIP backend, never part of it.
+ * TEST INFRASTRUCTURE ONLY: the oracle for the HIP backend, never part of it.
  * Citations are file:line in the gemma4-rs repository.  Build flags matter:
  * -ffp-contract=off keeps every a*b+c as two rounded operations, as rustc
  * emits them; the libm calls (expf, sinf, cosf, powf, sqrtf) are the

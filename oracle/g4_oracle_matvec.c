@@ -3,7 +3,7 @@
  * GGUF weight formats (crates/llm-backend-cpu/src/matvec.rs, dequant.rs) and
  * the activations applied to their results (crates/llm-backend-cpu/src/ops.rs).
  *
- * TEST INFRASTRUCTURE ONLY: the checker for the HIP backend, never part of it.
+ * TEST INFRASTRUCTURE ONLY: the oracle for the HIP backend, never part of it.
  * Built with -ffp-contract=off like the rest of the oracle: every product
  * and sum is its own rounded f32 operation, in the reference's order.
  */
