@@ -392,7 +392,7 @@ def main():
                          "plain 256 MiB device copy, the reference point for HBM byte counters")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: this build runs on a single MI355X (asked for --gpus {args.gpus}).",
+        print(f"bench.py measures one GPU: the backend runs on a single MI355X (asked for --gpus {args.gpus}).",
               file=sys.stderr)
         sys.exit(2)
 
