@@ -857,6 +857,10 @@ int g4_layer_attention(g4_ctx *ctx, g4_kv_cache *cache, const g4_hparams *hp, in
             rc = prepare_checks(ctx, q, owner ? k : nullptr, v, 1, position, hp->n_heads, hp->n_kv_heads, head_dim,
                                 hp->rms_norm_eps, pl.base, nullptr, nullptr, row_width);
             if (rc != G4_OK) return rc;
+            // The appended row is counted before the launch: the window's
+            // view includes it.
+            const int64_t rows_before = layer < cache->n_layers ? cache->rows[layer] : 0;
+            const int known_before = cache->known_layers;
             if (owner) {
                 rc = owner_rows(cache, layer, row_width, 1, &k_rows, &v_rows);
                 if (rc != G4_OK) return rc;
@@ -865,14 +869,35 @@ int g4_layer_attention(g4_ctx *ctx, g4_kv_cache *cache, const g4_hparams *hp, in
             const float *keys = nullptr, *values = nullptr;
             int64_t stride = 0;
             rc = g4_kv_view_rows(cache, pl.source, begin, end, &keys, &values, &stride);
-            if (rc != G4_OK) return rc;
-            if (stride != row_width)
-                return invalid("g4_layer_attention: source layer's row width differs from this layer's");
+            if (rc == G4_OK && stride != row_width)
+                rc = invalid("g4_layer_attention: source layer's row width differs from this layer's");
+            if (rc != G4_OK) {
+                // The reference appends, then fails at the view (model.rs:405-407):
+                // the row is written and stays counted.
+                if (owner) {
+                    const int saved = rc;
+                    const std::string msg = g4_last_error();
+                    uint64_t fa = 0, fb = 0;
+                    g4_last_error_fields(&fa, &fb);
+                    rc = prepare(ctx, q, k, v, 1, position, hp->n_heads, hp->n_kv_heads, head_dim, q_norm_w, k_norm_w,
+                                 hp->rms_norm_eps, pl.base, pl.factors, k_rows, v_rows, row_width, as_stream(stream));
+                    if (rc == G4_OK) rc = mirror_rows(cache, layer, position, 1, as_stream(stream));
+                    if (rc != G4_OK) return rc;
+                    return g4::set_error(saved, msg, fa, fb);
+                }
+                return rc;
+            }
             // model.rs:409-410: q and k are RMS-normalised, so the scale is 1.0.
             rc = decode_step_fused(ctx, q, owner ? k : nullptr, v, q_norm_w, k_norm_w, hp->rms_norm_eps, pl.base,
                                    pl.factors, position, keys, values, stride, end - begin, k_rows, v_rows,
                                    hp->n_heads, hp->n_kv_heads, head_dim, 1.0f, out, as_stream(stream));
-            if (rc != G4_OK) return rc;
+            if (rc != G4_OK) {  // a launch failure: the row was not written
+                if (owner) {
+                    cache->rows[layer] = rows_before;
+                    cache->known_layers = known_before;
+                }
+                return rc;
+            }
             return owner ? mirror_rows(cache, layer, position, 1, as_stream(stream)) : (int)G4_OK;
         }
         // Other shapes: model.rs:394-406 in one preparation launch (q norm +

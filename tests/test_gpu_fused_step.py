@@ -98,3 +98,68 @@ def test_fused_step_rejects_other_shapes(ctx):
     with pytest.raises(g4hip.EngError, match="n_rows"):
         ctx.decode_step_fused(z, None, None, None, None, EPS, 10000.0, None, 3, K, K, d, n, None, None, 8, 1, 256,
                               torch.zeros(8 * 256, device="cuda"))
+
+
+def _copy_out(ptr, n):
+    """n floats at device address ptr (hipMemcpy, test plumbing)."""
+    import ctypes
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    out = np.zeros(n, np.float32)
+    assert hip.hipMemcpy(out.ctypes.data, ptr, 4 * n, 2) == 0  # hipMemcpyDeviceToHost
+    return out
+
+
+@pytest.mark.parametrize("layer", [0, 4])
+def test_layer_attention_past_the_cache_fails_like_the_reference(ctx, layer):
+    """model.rs:394-407 appends the new row, then views position + 1 rows: a
+    position past the cached rows fails at the view with ContextTooLong and
+    leaves the appended row in the cache.  The device cache must end in the
+    same state as the oracle's: same error fields, same length, same row."""
+    import g4hip
+    print(f"[case] layer_attention past the cache, layer {layer}", flush=True)
+    hp_g = g4hip.G4Hparams(7, 8, 1, 256, 512, 16, 2, 10000.0, 1000000.0, 1e-6)
+    hp_o = orc.Hparams(7, 8, 1, 256, 512, 16, 2, 10000.0, 1000000.0, 1e-6)
+    d = 512 if layer == 4 else 256
+    rng = np.random.default_rng(40 + layer)
+    freqs = I.rope_freqs(7, 512)
+    cache = g4hip.KvCache(ctx, [256, 256, 256, 256, 512], 64)
+    ocache = orc.KvCache()
+    try:
+        hist = 3
+        K = rng.standard_normal((hist, d)).astype(np.float32)
+        V = rng.standard_normal((hist, d)).astype(np.float32)
+        cache.append_rows(layer, dev(K), dev(V), hist)
+        for t in range(hist):
+            ocache.append(layer, K[t], V[t])
+        q, k, v = (rng.standard_normal(m * d).astype(np.float32) for m in (8, 1, 1))
+        wq, wk = (rng.uniform(0.5, 1.5, d).astype(np.float32) for _ in range(2))
+        f = freqs if d == 512 else None
+        pos = 10
+        with pytest.raises(orc.OracleError) as oe:
+            ocache.layer_attention(hp_o, layer, pos, q, k, v, wq, wk, f)
+        out = torch.zeros(8 * d, device="cuda")
+        with pytest.raises(g4hip.EngError) as ge:
+            cache.layer_attention(hp_g, layer, pos, dev(q), dev(k), dev(v), dev(wq), dev(wk),
+                                  dev(f) if f is not None else None, out)
+        ctx.check_status()
+        assert ge.value.kind == "ContextTooLong" and oe.value.code == 2
+        assert ge.value.message == oe.value.message == "context length 11 exceeds configured max 4"
+        assert ge.value.fields == (11, 4)
+        assert cache.len(layer) == hist + 1
+        ok, ov = ocache.view(layer, hist + 1)
+        kp, vp, stride = cache.view(layer, hist + 1)
+        gk = _copy_out(kp, (hist + 1) * d).reshape(hist + 1, d)
+        gv = _copy_out(vp, (hist + 1) * d).reshape(hist + 1, d)
+        assert np.array_equal(gk[:hist], ok[:hist]) and np.array_equal(gv, ov)  # V has no RoPE: bit-exact
+        assert np.max(np.abs(gk[hist] - ok[hist])) < 2e-5  # device sin/cos vs host libm, same angles
+        # the cache keeps working: the next position attends all five rows
+        q, k, v = (rng.standard_normal(m * d).astype(np.float32) for m in (8, 1, 1))
+        ref, src, rr, _, _, _ = ocache.layer_attention(hp_o, layer, hist + 1, q, k, v, wq, wk, f)
+        gsrc, grange = cache.layer_attention(hp_g, layer, hist + 1, dev(q), dev(k), dev(v), dev(wq), dev(wk),
+                                             dev(f) if f is not None else None, out)
+        ctx.check_status()
+        assert (gsrc, grange) == (src, rr) and cache.len(layer) == hist + 2
+        assert I.rel_err(host(out), ref) <= TOL
+    finally:
+        cache.close()
