@@ -820,6 +820,9 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeK p) {
         for (int b = 0; b < kMergeBatch; ++b) t[b] = p.part_ml[slot(min(j0 + 16 * b, n - 1)) * G + c];
 #pragma unroll
         for (int b = 0; b < kMergeBatch; ++b) v[b] = ((const f32x4 *)(p.part_o + slot(min(j0 + 16 * b, n - 1)) * G * D))[e];
+        // No wait before every load above is issued: left alone, the
+        // scheduler trickled the vector loads out between the folds.
+        __builtin_amdgcn_sched_barrier(0);
         fold_batch(mt, lt, ot, t, v, j0, 16, n);
     }
     // Phases 4w..4w+3 of wave w sit 16 lanes apart.

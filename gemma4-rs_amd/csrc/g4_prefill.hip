@@ -473,38 +473,54 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillK p) {
     __shared__ float Linv[kRowsPerWave];
     __shared__ float tr[kRowsPerWave * DH];
     const int n = bi.n_units;
+    // Every load first (one memory round trip): the wave's (m, l) per row and
+    // unit, and this thread's partial vectors.  Units j >= n reload unit n-1
+    // (unconditional loads, no wait between them) and are zeroed when used.
+    constexpr int NE = NT * 64 / 256;  // vectors per thread
+    static_assert(NT * 64 % 256 == 0, "whole vectors per thread");
+    const int row = rg * kRowsPerWave + (tid & (kRowsPerWave - 1));
+    float2 ml[kPrefillMaxUnitsDev];
+#pragma unroll
+    for (int j = 0; j < kPrefillMaxUnitsDev; ++j)
+        ml[j] = p.part_ml[((int64_t)(bi.first_slot + min(j, n - 1)) * gridDim.y + kvh) * 64 + row];
+    const int64_t slot_stride = (int64_t)gridDim.y * kWaves * kRowsPerWave * D / 4;  // f32x4
+    const f32x4 *base = (const f32x4 *)p.part_o +
+                        ((int64_t)bi.first_slot * gridDim.y + kvh) * (kWaves * kRowsPerWave * D / 4) +
+                        (int64_t)wave * NT * 64;
+    f32x4 v[NE][kPrefillMaxUnitsDev];
+#pragma unroll
+    for (int k = 0; k < NE; ++k)
+#pragma unroll
+        for (int j = 0; j < kPrefillMaxUnitsDev; ++j)
+            v[k][j] = base[min(j, n - 1) * slot_stride + tid + 256 * k];
+    __builtin_amdgcn_sched_barrier(0);  // no wait before every load above is issued
     if (tid < kRowsPerWave) {
-        const int row = rg * kRowsPerWave + tid;
         float M = -INFINITY;
-        for (int j = 0; j < n; ++j)
-            M = fmaxf(M, p.part_ml[((int64_t)(bi.first_slot + j) * gridDim.y + kvh) * 64 + row].x);
+#pragma unroll
+        for (int j = 0; j < kPrefillMaxUnitsDev; ++j)
+            if (j < n) M = fmaxf(M, ml[j].x);
         float L = 0.0f;
+#pragma unroll
         for (int j = 0; j < kPrefillMaxUnitsDev; ++j) {
             float wj = 0.0f;
             if (j < n) {
-                const float2 ml = p.part_ml[((int64_t)(bi.first_slot + j) * gridDim.y + kvh) * 64 + row];
-                wj = ml.x == -INFINITY ? 0.0f : exp2_fast((ml.x - M) * kLog2e);
-                L += wj * ml.y;
+                wj = ml[j].x == -INFINITY ? 0.0f : exp2_fast((ml[j].x - M) * kLog2e);
+                L += wj * ml[j].y;
             }
             w[j][tid] = wj;
         }
         Linv[tid] = 1.0f / L;
     }
     __syncthreads();
-    const int64_t slot_stride = (int64_t)gridDim.y * kWaves * kRowsPerWave * D / 4;  // f32x4
-    const f32x4 *base = (const f32x4 *)p.part_o +
-                        ((int64_t)bi.first_slot * gridDim.y + kvh) * (kWaves * kRowsPerWave * D / 4) +
-                        (int64_t)wave * NT * 64;
-    for (int e = tid; e < NT * 64; e += 256) {
+#pragma unroll
+    for (int k = 0; k < NE; ++k) {
+        const int e = tid + 256 * k;
         const int lane = e & 63, tile = e >> 6;
         const int g = lane >> 4, c = lane & 15;
-        f32x4 v[kPrefillMaxUnitsDev];
-#pragma unroll
-        for (int j = 0; j < kPrefillMaxUnitsDev; ++j)  // n is uniform: scalar branches, no idle loads
-            v[j] = j < n ? base[j * slot_stride + e] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int j = 0; j < kPrefillMaxUnitsDev; ++j) acc += w[j][c] * v[j];
+        for (int j = 0; j < kPrefillMaxUnitsDev; ++j)
+            acc += w[j][c] * (j < n ? v[k][j] : f32x4{0.0f, 0.0f, 0.0f, 0.0f});
         const int U = tile >> 2, i = tile & 3;
         const float inv = Linv[c];
 #pragma unroll
