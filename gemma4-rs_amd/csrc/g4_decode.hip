@@ -305,13 +305,18 @@ struct DecodeAcc {
     f32x4 o[TW];
     bool bad;  // a NaN or +inf score was seen
 
-    __device__ __forceinline__ void start(const L &ln, const float *q_row, bool col_valid) {
+    // q_row: head c's row, or for a padding column (c >= group) any real
+    // head's.  MFMA output columns do not mix, a padding column's softmax
+    // state only gates the shared rescale branch (its alpha is its own), and
+    // its results and flags are never written, so the loaded row is used
+    // as is: no select waits on the load before the K/V loads are issued.
+    __device__ __forceinline__ void start(const L &ln, const float *q_row) {
         const float *qh = q_row + ln.base + 4 * ln.g;
 #pragma unroll
         for (int u = 0; u < KU; ++u) {
             const f32x4 a = *(const f32x4 *)(qh + 16 * u);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) qreg[u][j] = col_valid ? a[j] : 0.0f;
+            for (int j = 0; j < 4; ++j) qreg[u][j] = a[j];
         }
         m = -INFINITY;
         l = 0.0f;
@@ -515,6 +520,9 @@ __device__ __forceinline__ void run_pairs(const DecodeLane<D> &ln, DecodeAcc<D> 
                                           float scale, PairScores<D> &sx, int &buf) {
     PairPipe<D, NBUF, AUX> pp;
     if (n_keys - 32 * q_first <= 16) {  // a single tile: its second half is not computed
+        // The scheduler issues the K loads ahead of the score chain and the V
+        // loads after it, so the scores overlap the V transfer; issuing all
+        // eight loads at once measured slower (4096 keys: 10.3 -> 11.2 us).
         ln.template load_tile<AUX>(krs, vrs, 2 * q_first, pp.T[0][0]);
         acc.template pair<1>(ln, pp.T[0], n_keys - 32 * q_first, scale, sx, buf);
         return;
@@ -556,7 +564,7 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::NW) void decode_split_kernel(D
     const int head = kvh * p.group + (col_valid ? ln.c : 0);
     DecodeAcc<D> acc;
     acc.bad = false;
-    acc.start(ln, p.q + ((int64_t)s * p.n_heads + head) * D, col_valid);
+    acc.start(ln, p.q + ((int64_t)s * p.n_heads + head) * D);
     __shared__ PairScores<D> sx;
     int buf = 0;
     run_pairs<D, NBUF, AUX>(ln, acc, krs, vrs, 0, n_pairs, n_keys, p.scale, sx, buf);
@@ -636,7 +644,7 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::NW) void decode_layer_kernel(D
     const int hc = col_valid ? ln.c : 0;
     DecodeAcc<D> acc;
     acc.bad = false;
-    acc.start(ln, qp[hc], col_valid);
+    acc.start(ln, qp[hc]);
     __shared__ PairScores<D> sx;
     int buf = 0;
     if (n_keys > 0) {
@@ -757,7 +765,7 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::NW) void decode_stream_kernel(
         const int64_t first = row_at(cs) * p.row_stride + (int64_t)kvh * D;
         const __amdgpu_buffer_rsrc_t krs = ln.rows(p.k + first, n_keys, stride);
         const __amdgpu_buffer_rsrc_t vrs = ln.rows(p.v + first, n_keys, stride);
-        acc.start(ln, p.q + ((int64_t)cs * p.n_heads + head) * D, col_valid);
+        acc.start(ln, p.q + ((int64_t)cs * p.n_heads + head) * D);
         run_pairs<D, NBUF, 0>(ln, acc, krs, vrs, g - ga, ge - g, n_keys, p.scale, sx, buf);
         if (g == ga && ge == gb) {
             acc.write_output(ln, p.out + ((int64_t)cs * p.n_heads + head) * D, col_valid, p.status);
