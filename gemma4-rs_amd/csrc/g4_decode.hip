@@ -780,16 +780,39 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::NW) void decode_stream_kernel(
 }
 
 // Merges the split partials of one (sequence, KV head):
+// Folds splits ph, ph + PH, ... < n of stored vector e into (m, l, o), NB
+// splits per batch: every load of a batch is issued before any is used.
+// Partial j sits at slot0 + j*jslot, plus first_extra for j = 0.
+template <int D, int PH, int NB>
+__device__ __forceinline__ void merge_fold(const DecodeK &p, int64_t slot0, int64_t jslot, int64_t first_extra,
+                                           int ph, int e, int c, int n, int G, float &m, float &l, f32x4 &o) {
+    auto slot = [&](int j) { return slot0 + j * jslot + (j == 0 ? first_extra : 0); };
+    for (int j0 = ph; j0 < n; j0 += PH * NB) {
+        float2 t[NB];
+        f32x4 v[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) t[b] = p.part_ml[slot(min(j0 + PH * b, n - 1)) * G + c];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) v[b] = ((const f32x4 *)(p.part_o + slot(min(j0 + PH * b, n - 1)) * G * D))[e];
+        // No wait before every load above is issued: left alone, the
+        // scheduler trickled the vector loads out between the folds.
+        __builtin_amdgcn_sched_barrier(0);
+        fold_batch(m, l, o, t, v, j0, PH, n);
+    }
+}
+
 // O_c = sum_j e^(m_jc - M_c) O_jc / sum_j e^(m_jc - M_c) l_jc for each head c.
-// A workgroup covers EPW stored vectors; its PH = 256/EPW thread phases each
-// fold every PH-th split into a running partial in registers, NB splits per
-// batch (all of a batch's loads are issued before any is used), then the
-// phases are combined across lanes and waves in a fixed order
-// (deterministic), and EPW lanes write the result.
-template <int MODE, int D, int EPW, int NB>
+// A workgroup covers EPW stored vectors of one (sequence, KV head); its
+// PH = 256/EPW thread phases each fold every PH-th split into a running
+// partial in registers, then the phases are combined across lanes and waves
+// in a fixed order (deterministic), and EPW lanes write the result.  The
+// split count n is uniform in the workgroup: the batch size is the smallest
+// that covers n in one memory round trip (up to 256 splits), so no lane
+// reloads a split it does not use.
+template <int MODE, int D, int EPW>
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeK p) {
     constexpr int PH = 256 / EPW;
-    static_assert(EPW >= 8 && EPW <= 16 && NB >= 1, "whole 128-byte rows per phase; at most 16 lanes write");
+    static_assert(EPW == 8 || EPW == 16, "whole 128-byte rows per phase; at most 16 lanes write");
     const int s = blockIdx.z, kvh = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     int n = p.max_splits;
@@ -814,27 +837,25 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeK p) {
         n = (int)num_splits(p, len);
     }
     if (MODE != kSingle && n <= 1) return;  // kSingle: launched only with splits
+    n = __builtin_amdgcn_readfirstlane(n);
     const int G = p.group;
 
     const int ph = tid / EPW, el = tid % EPW;
     const int e = blockIdx.x * EPW + el;  // stored vector index within a split
     const int c = e % G;
-    auto slot = [&](int j) { return slot0 + j * jslot + (j == 0 ? first_extra : 0); };
 
     float mt = -INFINITY, lt = 0.0f;
     f32x4 ot = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int j0 = ph; j0 < n; j0 += PH * NB) {
-        float2 t[NB];
-        f32x4 v[NB];
-#pragma unroll
-        for (int b = 0; b < NB; ++b) t[b] = p.part_ml[slot(min(j0 + PH * b, n - 1)) * G + c];
-#pragma unroll
-        for (int b = 0; b < NB; ++b) v[b] = ((const f32x4 *)(p.part_o + slot(min(j0 + PH * b, n - 1)) * G * D))[e];
-        // No wait before every load above is issued: left alone, the
-        // scheduler trickled the vector loads out between the folds.
-        __builtin_amdgcn_sched_barrier(0);
-        fold_batch(mt, lt, ot, t, v, j0, PH, n);
-    }
+    if (n <= PH)
+        merge_fold<D, PH, 1>(p, slot0, jslot, first_extra, ph, e, c, n, G, mt, lt, ot);
+    else if (n <= 2 * PH)
+        merge_fold<D, PH, 2>(p, slot0, jslot, first_extra, ph, e, c, n, G, mt, lt, ot);
+    else if (n <= 4 * PH)
+        merge_fold<D, PH, 4>(p, slot0, jslot, first_extra, ph, e, c, n, G, mt, lt, ot);
+    else if (n <= 8 * PH || EPW == 8)
+        merge_fold<D, PH, 8>(p, slot0, jslot, first_extra, ph, e, c, n, G, mt, lt, ot);
+    else
+        merge_fold<D, PH, 16>(p, slot0, jslot, first_extra, ph, e, c, n, G, mt, lt, ot);
     // The phases of wave w sit EPW lanes apart.
 #pragma unroll
     for (int off = EPW; off <= 32; off <<= 1) {
@@ -961,35 +982,27 @@ int launch_stream(g4_ctx *ctx, const DecodeArgs &a, DecodeK p, hipStream_t strea
     G4_HIP(hipGetLastError());
     const dim3 mgrid(D * G / 64, a.n_kv_heads, a.B);
     if (D == 256)
-        hipLaunchKernelGGL((decode_merge_kernel<kStream, 256, 16, 16>), mgrid, dim3(256), 0, stream, p);
+        hipLaunchKernelGGL((decode_merge_kernel<kStream, 256, 16>), mgrid, dim3(256), 0, stream, p);
     else
-        hipLaunchKernelGGL((decode_merge_kernel<kStream, 512, 16, 16>), mgrid, dim3(256), 0, stream, p);
+        hipLaunchKernelGGL((decode_merge_kernel<kStream, 512, 16>), mgrid, dim3(256), 0, stream, p);
     G4_HIP(hipGetLastError());
     return G4_OK;
 }
 
 // lp: the fused layer step (one sequence), launched as decode_layer_kernel
 // with the split kernel's sizing.
-template <int MODE, int D, int EPW, int NB>
-void launch_merge_shape(const DecodeK &p, int group, int n_kv_heads, int B, hipStream_t stream) {
-    hipLaunchKernelGGL((decode_merge_kernel<MODE, D, EPW, NB>), dim3(D * group / 4 / EPW, n_kv_heads, B), dim3(256), 0,
-                       stream, p);
-}
-
-// The merge's shape for n splits.  One sequence: a single batch covers all
-// n splits (one memory round trip, no reloads); up to 64 splits with 16
-// vectors per workgroup (fewer shuffle rounds), more with 8 (twice the
-// workgroups to share the bytes).  Measured on one sequence: 32 splits at
-// d=256 7.2 -> 6.2 us per step, 256 splits at d=512 10.3 -> 9.9 us.
-// Batches keep 16 vectors and 16-split batches.
+// The merge's workgroup width for n splits: one sequence above 64 splits
+// takes 8 vectors per workgroup (twice the workgroups to share the bytes),
+// otherwise 16 (fewer shuffle rounds).  Measured on one sequence: 32 splits
+// at d=256 7.2 -> 6.2 us per step, 256 splits at d=512 10.3 -> 9.9 us.
 template <int MODE, int D>
 void launch_merge(const DecodeK &p, int64_t n, int group, int n_kv_heads, int B, hipStream_t stream) {
-    if (MODE != kSingle) return launch_merge_shape<MODE, D, 16, 16>(p, group, n_kv_heads, B, stream);
-    if (n <= 16) return launch_merge_shape<MODE, D, 16, 1>(p, group, n_kv_heads, B, stream);
-    if (n <= 32) return launch_merge_shape<MODE, D, 16, 2>(p, group, n_kv_heads, B, stream);
-    if (n <= 64) return launch_merge_shape<MODE, D, 16, 4>(p, group, n_kv_heads, B, stream);
-    if (n <= 128) return launch_merge_shape<MODE, D, 8, 4>(p, group, n_kv_heads, B, stream);
-    launch_merge_shape<MODE, D, 8, 8>(p, group, n_kv_heads, B, stream);
+    if (MODE == kSingle && n > 64)
+        hipLaunchKernelGGL((decode_merge_kernel<MODE, D, 8>), dim3(D * group / 32, n_kv_heads, B), dim3(256), 0,
+                           stream, p);
+    else
+        hipLaunchKernelGGL((decode_merge_kernel<MODE, D, 16>), dim3(D * group / 64, n_kv_heads, B), dim3(256), 0,
+                           stream, p);
 }
 
 template <int MODE>
