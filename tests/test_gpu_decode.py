@@ -50,11 +50,14 @@ def test_decode_lengths(ctx, d, T):
     assert I.rel_err(out, orc.attend(q, K, V, 8, 1)) <= TOL
 
 
-@pytest.mark.parametrize("chunk", [16, 32, 48, 256, 4096])
-def test_decode_split_counts(ctx, chunk):
-    """Split-K partials merge to the same result for any split size."""
-    T, d = 3000, 512
-    q, K, V, _ = I.decode_case(55, T, d, True)
+@pytest.mark.parametrize("T,chunk", [(3000, 16), (3000, 32), (3000, 48), (3000, 256), (3000, 4096), (5000, 16),
+                                     (1500, 16), (700, 16)])
+def test_decode_split_counts(ctx, T, chunk):
+    """Split-K partials merge to the same result for any split size: the
+    merge's shapes for 44, 47, 94, 188 and 313 splits (two batches), and
+    a single split."""
+    d = 512
+    q, K, V, _ = I.decode_case(55 + T, T, d, True)
     ctx.set_decode_chunk(chunk)
     try:
         out = run_decode(ctx, q, K, V, 0, T, 8, 1, d)
@@ -236,13 +239,16 @@ def test_ragged_batch_shapes(ctx, name, lens, d, n_heads, n_kv):
     assert worst <= TOL
 
 
-def test_ragged_batch_with_set_split_size(ctx):
-    """A split size set by the caller selects the per-sequence split grid."""
-    lens = np.array([1500, 20, 333, 4096, 1], np.int64)
+@pytest.mark.parametrize("chunk", [64, 16])
+def test_ragged_batch_with_set_split_size(ctx, chunk):
+    """A split size set by the caller selects the per-sequence split grid;
+    the merge folds 1 to 313 splits per sequence (at 16 keys: 94, 2, 21,
+    256 and 313, the last in two batches)."""
+    lens = np.array([1500, 20, 333, 4096, 1, 5000], np.int64)
     d = 512
     q, K, V, row0 = _ragged_case(77, lens, d)
     out = torch.zeros(len(lens) * 8 * d, device="cuda")
-    ctx.set_decode_chunk(64)
+    ctx.set_decode_chunk(chunk)
     try:
         ctx.attend_decode_batch(dev(q), dev(K), dev(V), dev(row0), dev(np.zeros(len(lens), np.int64)), dev(lens),
                                 int(lens.max()), 8, 1, d, out)
