@@ -606,6 +606,25 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::NW) void decode_layer_kernel(D
     const int rows = n_keys > 0 ? n_keys : 1;  // with no key to read the resources go unused
     const __amdgpu_buffer_rsrc_t krs = ln.rows(p.k + first, rows, stride);
     const __amdgpu_buffer_rsrc_t vrs = ln.rows(p.v + first, rows, stride);
+    // The preparation's loads first, then the K/V loads: memory counters
+    // complete in issue order, so the preparation then waits only for its
+    // own (small, mostly cached) rows and runs while the K/V tiles stream.
+    // Wavefront w takes query head kvh*NW + w; in the fresh workgroup waves
+    // 0 and 1 also take the new row's k and v.
+    static_assert(D / 2 <= kPrepMaxAngles, "the angle table covers the head");
+    __shared__ float qp[NW][D];
+    __shared__ float kvn[2][D];
+    __shared__ float sk[NW];
+    const bool is_k = ln.wave == 0, prep_kv = fresh && ln.wave < 2;
+    PrepRow<D> row, kv;
+    prep_load<D>(row, ln.lane, lp.q + ((int64_t)kvh * NW + ln.wave) * D, lp.q_w, lp.factors, true);
+    prep_load_angles<D>(row, ln.lane, lp.angles);
+    if (prep_kv) {
+        prep_load<D>(kv, ln.lane, (is_k ? lp.k : lp.v) + (int64_t)kvh * D, is_k ? lp.k_w : nullptr, lp.factors,
+                     is_k);
+        if (is_k) prep_load_angles<D>(kv, ln.lane, lp.angles);
+    }
+    __builtin_amdgcn_sched_barrier(0);
     PairPipe<D, NBUF, AUX> pp;
     if (n_keys > 0) {
         if (single)
@@ -613,26 +632,11 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::NW) void decode_layer_kernel(D
         else
             pp.prime(ln, krs, vrs, 0, n_pairs);
     }
-
-    // The preparation, while those loads are in flight: wavefront w takes
-    // query head kvh*NW + w; in the fresh workgroup waves 0 and 1 then take
-    // the new row's k and v.
-    static_assert(D / 2 <= kPrepMaxAngles, "the angle table covers the head");
-    __shared__ float qp[NW][D];
-    __shared__ float kvn[2][D];
-    __shared__ float sk[NW];
+    __builtin_amdgcn_sched_barrier(0);
     {
-        PrepRow<D> row;
-        prep_load<D>(row, ln.lane, lp.q + ((int64_t)kvh * NW + ln.wave) * D, lp.q_w, lp.factors, true);
-        prep_load_angles<D>(row, ln.lane, lp.angles);
         prep_compute<D>(row, lp.q_w != nullptr, true, lp.eps);
         prep_store<D>(row, ln.lane, qp[ln.wave]);
-        if (fresh && ln.wave < 2) {
-            const bool is_k = ln.wave == 0;
-            PrepRow<D> kv;
-            prep_load<D>(kv, ln.lane, (is_k ? lp.k : lp.v) + (int64_t)kvh * D, is_k ? lp.k_w : nullptr, lp.factors,
-                         is_k);
-            if (is_k) prep_load_angles<D>(kv, ln.lane, lp.angles);
+        if (prep_kv) {
             prep_compute<D>(kv, is_k && lp.k_w != nullptr, is_k, lp.eps);
             prep_store<D>(kv, ln.lane, kvn[ln.wave]);
             prep_store<D>(kv, ln.lane, (is_k ? lp.k_row : lp.v_row) + (int64_t)kvh * D);  // the append
