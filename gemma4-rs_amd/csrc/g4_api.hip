@@ -341,8 +341,11 @@ int g4_attend(g4_ctx *ctx, const float *q_host, size_t q_len, const float *keys_
         if (n_heads == 0 || n_kv_heads == 0) return invalid("attention needs positive head counts");
         const size_t head_dim = q_len / n_heads;
         if (head_dim == 0) return invalid("q is shorter than n_heads");
-        // model.rs:362-364: an empty context fails the softmax of every head.
-        if (T == 0) return g4::set_error(G4_ERR_COMPUTE, "softmax input is not finite");
+        // model.rs:362-364: an empty context fails the softmax of every head,
+        // and a q whose length is not n_heads * head_dim leaves the heads'
+        // concatenation shorter than q; both return this error.
+        if (T == 0 || q_len != n_heads * head_dim)
+            return g4::set_error(G4_ERR_COMPUTE, "softmax input is not finite");
         const size_t width = n_kv_heads * head_dim;
         const size_t used_q = n_heads * head_dim;
         G4_HIP(hipSetDevice(ctx->device));
@@ -850,7 +853,14 @@ int g4_layer_attention(g4_ctx *ctx, g4_kv_cache *cache, const g4_hparams *hp, in
         da.n_kv_heads = hp->n_kv_heads;
         da.head_dim = head_dim;
         float *k_rows = nullptr, *v_rows = nullptr;
-        if (g4::layer_decode_fusable(da)) {
+        // The append pushes the new row after the cached ones (row
+        // rows_before, context_memory.rs:44-51) and the view takes the first
+        // position + 1 rows: the new row is the view's last one only when
+        // rows_before == position.  Otherwise (a cache longer or shorter than
+        // the position) the two-step path below appends and views as the
+        // reference does.
+        const int64_t rows_before = layer < cache->n_layers ? cache->rows[layer] : 0;
+        if (g4::layer_decode_fusable(da) && (!owner || rows_before == position)) {
             // One launch (plus the split merge): the decode kernel prepares q
             // and, on an owner layer, the new row, which it appends and
             // attends (model.rs:394-410).  q, k and v are left as given.
@@ -859,7 +869,6 @@ int g4_layer_attention(g4_ctx *ctx, g4_kv_cache *cache, const g4_hparams *hp, in
             if (rc != G4_OK) return rc;
             // The appended row is counted before the launch: the window's
             // view includes it.
-            const int64_t rows_before = layer < cache->n_layers ? cache->rows[layer] : 0;
             const int known_before = cache->known_layers;
             if (owner) {
                 rc = owner_rows(cache, layer, row_width, 1, &k_rows, &v_rows);
@@ -881,7 +890,7 @@ int g4_layer_attention(g4_ctx *ctx, g4_kv_cache *cache, const g4_hparams *hp, in
                     g4_last_error_fields(&fa, &fb);
                     rc = prepare(ctx, q, k, v, 1, position, hp->n_heads, hp->n_kv_heads, head_dim, q_norm_w, k_norm_w,
                                  hp->rms_norm_eps, pl.base, pl.factors, k_rows, v_rows, row_width, as_stream(stream));
-                    if (rc == G4_OK) rc = mirror_rows(cache, layer, position, 1, as_stream(stream));
+                    if (rc == G4_OK) rc = mirror_rows(cache, layer, rows_before, 1, as_stream(stream));
                     if (rc != G4_OK) return rc;
                     return g4::set_error(saved, msg, fa, fb);
                 }
@@ -898,7 +907,7 @@ int g4_layer_attention(g4_ctx *ctx, g4_kv_cache *cache, const g4_hparams *hp, in
                 }
                 return rc;
             }
-            return owner ? mirror_rows(cache, layer, position, 1, as_stream(stream)) : (int)G4_OK;
+            return owner ? mirror_rows(cache, layer, rows_before, 1, as_stream(stream)) : (int)G4_OK;
         }
         // Other shapes: model.rs:394-406 in one preparation launch (q norm +
         // RoPE; on owner layers k/v norm, k RoPE and the append), then the

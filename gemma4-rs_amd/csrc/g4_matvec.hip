@@ -55,7 +55,15 @@ __device__ inline float half_bits_to_float(unsigned bits) {
     return (float)__builtin_bit_cast(_Float16, (unsigned short)(bits & 0xffffu));
 }
 
-__device__ inline float round_to_half(float x) { return (float)(_Float16)x; }
+// f16 rounding of an f32 value (half::f16::from_f32).  The empty asm makes
+// x opaque: otherwise the compiler fuses a product that feeds the conversion
+// into one mixed-precision fma (v_fma_mixlo_f16 a, b, 0), which rounds the
+// exact product to f16 once -- where the reference rounds it to f32 first --
+// and turns a -0 product into +0.
+__device__ inline float round_to_half(float x) {
+    asm volatile("" : "+v"(x));
+    return (float)(_Float16)x;
+}
 
 // Rust's `f32 as i8`: saturating, NaN -> 0.
 __device__ inline int saturate_i8(float v) {
@@ -406,7 +414,10 @@ int launch_q8(g4_ctx *ctx, MatvecArgs a, hipStream_t stream) {
     // matrices are (GGUF aligns tensor data to 32 bytes).
     const bool aligned = ((uintptr_t)a.w % 16 == 0) && (NM == 1 || (uintptr_t)a.w2 % 16 == 0) &&
                          (a.xs || (uintptr_t)a.x % 16 == 0);
-    const bool fast = a.cols % 256 == 0 && nb <= 256 && aligned;
+    // An empty row (cols == 0) takes the row-wise kernel, which reads no
+    // block: the staged kernel loads the activation's blocks before it tests
+    // them against the block count.
+    const bool fast = a.cols % 256 == 0 && nb > 0 && nb <= 256 && aligned;
     // Rows per workgroup: up to 16, the product table under 16 KB.
     const int64_t rb_max = std::min<int64_t>(16, std::max<int64_t>(1, 16384 / (NM * (nb + 1) * 4)));
     const bool large = a.rows >= rb_max * 8 * num_cus;

@@ -188,6 +188,9 @@ __device__ __forceinline__ void prefill_unit(const PrefillK &p, const PrefillUni
     // latter.  The epilogue reuses the four tile arrays.
     __shared__ f32x4 lds_k0[TPS * TILE_F4], lds_v0[TPS * TILE_F4], lds_k1[TPS * TILE_F4], lds_v1[TPS * TILE_F4];
     __shared__ f32x4 lds_s0[S::WAVES][64], lds_s1[S::WAVES][64];
+    // Per wave group: 1 + the index of the last edge tile whose V held a
+    // non-finite value (see step()).
+    __shared__ int nf_tile[S::KSPLIT];
 
     // K/V tiles go straight from memory to LDS (buffer_load ... lds: lane l
     // of a wavefront writes the 16 bytes it loads to LDS base + 16*l), so the
@@ -258,7 +261,12 @@ __device__ __forceinline__ void prefill_unit(const PrefillK &p, const PrefillUni
     // Tiles t .. t+TPS-1 are read from (kb, vb) -- tile t+j at j*TILE_F4, by
     // the wave group of parity j -- while the next step's tiles load into
     // (kn, vn).
-    auto step = [&](int t, const f32x4 *kb, const f32x4 *vb, f32x4 (*ls)[64], f32x4 *kn, f32x4 *vn) {
+    // Tile tt is in the unit and every row of the block attends all of its
+    // keys (key <= P0 and, with a window, key > P0 + 7 - W).
+    auto exact = [&](int tt) {
+        return tt < u.t_hi && 16LL * tt + 15 <= P0 && (win == 0 || 16LL * tt > P0 + kPosPerBlock - 1 - win);
+    };
+    auto step = [&](int t, const f32x4 *kb, f32x4 *vb, f32x4 (*ls)[64], f32x4 *kn, f32x4 *vn) {
         // This step's tiles have landed (this wave's loads, then everyone's),
         // and every wave is done reading (kn, vn): fetch the next tiles into
         // them.  Past the unit's end the last tile is fetched again
@@ -273,7 +281,6 @@ __device__ __forceinline__ void prefill_unit(const PrefillK &p, const PrefillUni
         const int tw = t + kpar;
         const bool live = S::KSPLIT == 1 || tw < u.t_hi;  // one group: a step's tile is always live
         const f32x4 *kt = kb + kpar * TILE_F4;
-        const f32x4 *vt = vb + kpar * TILE_F4;
         constexpr int NL = 2 * PER_THREAD * TPS;  // tile-part loads per step
         // Partial S^T over this wave's DH dims: two independent chains.
         f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -322,7 +329,7 @@ __device__ __forceinline__ void prefill_unit(const PrefillK &p, const PrefillUni
         float sv[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) sv[r] = sc[r] * p.scale;
-        const bool whole = 16LL * tw + 15 <= P0 && (win == 0 || 16LL * tw > P0 + kPosPerBlock - 1 - win);
+        const bool whole = exact(tw) || !live;  // a stale tile is masked whole below
         if (!live) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) sv[r] = -INFINITY;
@@ -353,16 +360,84 @@ __device__ __forceinline__ void prefill_unit(const PrefillK &p, const PrefillUni
         for (int r = 0; r < 4; ++r) pr[r] = (m == -INFINITY) ? 0.0f : exp2_fast((sv[r] - m) * kLog2e);
         l += (pr[0] + pr[1]) + (pr[2] + pr[3]);
 
+        // Edge tiles: some row of the block masks keys of the tile that
+        // another row attends (or a wave group's tile is a stale one, every
+        // key masked).  A masked key's weight is exactly 0, but 0 * NaN and
+        // 0 * inf are NaN, and the reference multiplies only the rows a query
+        // attends (model.rs:339-341).  So the group's V tile has its
+        // non-finite values replaced by 0 in LDS before the product, and if
+        // it held any, their p * v terms are added afterwards, from memory, to
+        // the rows that attend them.  (Rows outside [block_lo, last_pos]
+        // already read as 0.)  Steps with no edge tile skip all of this.
+        bool fix = false;
+        if (!exact(t) || (TPS == 2 && !exact(t + 1))) {  // uniform in the workgroup
+            if (!(live && whole)) {
+                constexpr int GL = 64 * S::RWAVES;  // lanes of the waves sharing this V tile
+                f32x4 *vs = vb + kpar * TILE_F4;
+                const int gl = tid - kpar * GL;
+                bool found = false;
+#pragma unroll
+                for (int e = 0; e < TILE_F4 / GL; ++e) {
+                    f32x4 x = vs[e * GL + gl];
+                    bool bad4 = false;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) bad4 |= !__builtin_amdgcn_classf(x[i], 0x1F8);  // not -normal..+normal
+                    if (bad4) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            if (!__builtin_amdgcn_classf(x[i], 0x1F8)) x[i] = 0.0f;
+                        vs[e * GL + gl] = x;
+                        found = true;
+                    }
+                }
+                if (__any(found) && lane == 0) nf_tile[kpar] = tw + 1;
+            }
+            lds_barrier();  // the sanitized tile and the flag are visible to the group
+            // A flag left by an earlier unit with the same tile index only
+            // costs a fix-up pass that finds nothing.
+            fix = !(live && whole) && nf_tile[kpar] == tw + 1;
+        }
+
         // O^T += V^T . P^T over the tile's 16 keys (k-step r: keys 4g + r).
 #pragma unroll
         for (int r = 0; r < 4; ++r)
 #pragma unroll
             for (int U = 0; U < NV; ++U) {
-                const f32x4 vv = vt[(4 * g + r) * (D / 4) + d0 / 4 + 16 * U + c];
+                const f32x4 vv = vb[kpar * TILE_F4 + (4 * g + r) * (D / 4) + d0 / 4 + 16 * U + c];
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
                     o[4 * U + i] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[i], pr[r], o[4 * U + i], 0, 0, 0);
             }
+
+        if (fix) {
+            // Key k = 4kq + r of the tile: its weight for this lane's row c is
+            // pr[r] of lane (kq, c); it is attended iff k <= rel and (no
+            // window or k > rel - W).  O^T tile 4U + i, row 4g + r2 of this
+            // lane is dim d0 + 64U + 16g + 4r2 + i of row c.
+            const int64_t rel = pos - 16LL * tw;
+            for (int kq = 0; kq < 4; ++kq) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int k = 4 * kq + r;
+                    const float pk = __shfl(pr[r], kq * 16 + c);
+                    if (!(live && k <= rel && (win == 0 || k > rel - win))) continue;
+                    const uint32_t roff = (uint32_t)(((16LL * tw + k - block_lo) * stride + d0 + 16 * g) * 4);
+#pragma unroll
+                    for (int U = 0; U < NV; ++U)
+#pragma unroll
+                        for (int r2 = 0; r2 < 4; ++r2) {
+                            const f32x4 vv = __builtin_bit_cast(
+                                f32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, roff + (64 * U + 4 * r2) * 4, 0, 0));
+#pragma unroll
+                            for (int i = 0; i < 4; ++i)
+                                if (!__builtin_amdgcn_classf(vv[i], 0x1F8)) o[4 * U + i][r2] += pk * vv[i];
+                            // One load at a time: this path is rare, and hoisting
+                            // its loads would cost the hot loop registers.
+                            __builtin_amdgcn_sched_barrier(0);
+                        }
+                }
+            }
+        }
     };
 #pragma unroll
     for (int j = 0; j < TPS; ++j)

@@ -107,7 +107,7 @@ _SIGS = {
 
 
 class G4Hparams(ctypes.Structure):
-    """g4_hparams: the Gemma4HyperParams fields attention reads (idea/mod.rs:105-124)."""
+    """g4_hparams: the Gemma4HyperParams fields attention reads (idea/mod.rs:15-34)."""
 
     _fields_ = [
         ("n_layers", c_int), ("n_heads", c_int), ("n_kv_heads", c_int),
@@ -164,7 +164,7 @@ def _stream(stream):
 
 # ------------------------------------------------------------------ policies
 def layer_attention_kind(n_layers, layer):
-    """'global' or 'local' (crates/llm-gemma4/src/idea/mod.rs:238-246)."""
+    """'global' or 'local' (crates/llm-gemma4/src/idea/mod.rs:148-156)."""
     return "global" if lib().g4_layer_is_global(n_layers, layer) else "local"
 
 

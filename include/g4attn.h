@@ -177,7 +177,7 @@ int64_t g4_kv_len(const g4_kv_cache *cache, int layer);
 void g4_kv_clear(g4_kv_cache *cache); /* context_memory.rs:82-84 */
 
 /* --------------------------------------------------- layer attention driver */
-/* The Gemma4HyperParams fields attention reads (crates/llm-gemma4/src/idea/mod.rs:105-124). */
+/* The Gemma4HyperParams fields attention reads (crates/llm-gemma4/src/idea/mod.rs:15-34). */
 typedef struct {
     int n_layers, n_heads, n_kv_heads, head_dim_local, head_dim_global;
     int64_t sliding_window;
@@ -255,7 +255,7 @@ int g4_layer_prefill(g4_ctx *ctx, g4_kv_cache *cache, const g4_hparams *hp, int 
                      g4_stream stream);
 
 /* ----------------------------------------------------------- policies */
-/* layer_attention_kind (idea/mod.rs:238-246): 1 global, 0 local. */
+/* layer_attention_kind (idea/mod.rs:148-156): 1 global, 0 local. */
 int g4_layer_is_global(int n_layers, int layer);
 /* kv_source_layer (crates/llm-gemma4/src/eng/mod.rs:71-90); KvShareError ->
  * G4_ERR_COMPUTE with its Display text, as model.rs:398 maps it. */

@@ -307,7 +307,11 @@ static int attend_image(const float *q, size_t q_len, const float *keys, const f
         run_chunks(n_heads, work_per_head, ATTENTION_PARALLEL_MIN_WORK, attend_chunk, &c);
     else
         attend_chunk(&c, 0, n_heads);
-    if (atomic_load(&c.failed)) return fail(OR_ERR_COMPUTE, "softmax input is not finite");
+    /* model.rs:362-364: a failed head returns no values, and a q longer than
+     * n_heads * head_dim leaves the concatenation shorter than q; either way
+     * attended.len() != q.len(). */
+    if (atomic_load(&c.failed) || n_heads * head_dim != q_len)
+        return fail(OR_ERR_COMPUTE, "softmax input is not finite");
     return OR_OK;
 }
 
@@ -336,6 +340,62 @@ int or_attend_rows(const float *q, size_t q_len, const float *const *key_rows,
     free(kc);
     free(vc);
     return rc;
+}
+
+typedef struct {
+    const float *q, *keys, *values;
+    size_t q_len, N, pos0, window, n_heads, n_kv_heads, threads, width;
+    float scale;
+    int *status;
+    float *out;
+    atomic_int failed;
+    size_t index; /* this worker's first query */
+} prefill_ctx;
+
+static void *prefill_worker(void *arg) {
+    prefill_ctx *w = (prefill_ctx *)arg;
+    for (size_t i = w->index; i < w->N; i += w->threads) {
+        size_t begin, end;
+        /* generate.rs:37-41: token i runs as a decode at position pos0 + i. */
+        if (w->window)
+            or_windowed_len(w->pos0 + i + 1, w->window, &begin, &end);
+        else
+            begin = 0, end = w->pos0 + i + 1;
+        int rc = attend_image(w->q + i * w->q_len, w->q_len, w->keys + begin * w->width,
+                              w->values + begin * w->width, end - begin, w->n_heads, w->n_kv_heads,
+                              w->scale, 0, w->out + i * w->q_len);
+        if (w->status) w->status[i] = rc;
+        if (rc != OR_OK) atomic_store(&w->failed, 1);
+    }
+    return NULL;
+}
+
+int or_attend_prefill(const float *q, size_t q_len, size_t N, const float *keys, const float *values,
+                      size_t pos0, size_t window, size_t n_heads, size_t n_kv_heads, float scale,
+                      size_t threads, int *status, float *out) {
+    if (n_heads == 0 || threads == 0) return fail(OR_ERR_COMPUTE, "attend_prefill: zero heads or threads");
+    if (threads > 256) threads = 256;
+    prefill_ctx base = {q, keys, values, q_len, N, pos0, window, n_heads, n_kv_heads, threads,
+                        n_kv_heads * (q_len / n_heads), scale, status, out, 0, 0};
+    prefill_ctx w[256];
+    pthread_t th[256];
+    for (size_t t = 0; t < threads; ++t) {
+        w[t] = base;
+        w[t].index = t;
+    }
+    size_t started = 1;
+    for (size_t t = 1; t < threads; ++t, ++started)
+        if (pthread_create(&th[t], NULL, prefill_worker, &w[t]) != 0) break;
+    /* Queries of threads that could not start run here. */
+    for (size_t t = started; t < threads; ++t) prefill_worker(&w[t]);
+    prefill_worker(&w[0]);
+    int failed = atomic_load(&w[0].failed);
+    for (size_t t = 1; t < started; ++t) {
+        pthread_join(th[t], NULL);
+        failed |= atomic_load(&w[t].failed);
+    }
+    for (size_t t = started; t < threads; ++t) failed |= atomic_load(&w[t].failed);
+    return failed ? fail(OR_ERR_COMPUTE, "softmax input is not finite") : OR_OK;
 }
 
 /* f64 twin: same structure, double throughout (plain sequential sums). */
@@ -403,17 +463,17 @@ int or_rope_heads(float *x, size_t len, size_t head_dim, size_t position, float 
     return OR_OK;
 }
 
-/* idea/mod.rs:238-246 */
+/* idea/mod.rs:148-156 */
 int or_layer_attention_kind(size_t n_layers, size_t layer) {
     return (layer + 1 == n_layers || layer % 5 == 4) ? 1 : 0;
 }
 
-/* idea/mod.rs:230-235 */
+/* idea/mod.rs:140-145 */
 size_t or_head_dim(size_t n_layers, size_t layer, size_t head_dim_local, size_t head_dim_global) {
     return or_layer_attention_kind(n_layers, layer) ? head_dim_global : head_dim_local;
 }
 
-/* idea/mod.rs:252-255 -- `(head_dim as f32 * p / 2.0) as usize` pairs turn. */
+/* idea/mod.rs:162-165 -- `(head_dim as f32 * p / 2.0) as usize` pairs turn. */
 void or_proportional_rope_freq_factors(size_t head_dim, float p, float *out) {
     float r = (float)head_dim * p / 2.0f;
     size_t rotated = r > 0.0f ? (size_t)r : 0;

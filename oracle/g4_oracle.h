@@ -63,6 +63,18 @@ int or_attend(const float *q, size_t q_len, const float *keys, const float *valu
 int or_attend_rows(const float *q, size_t q_len, const float *const *key_rows,
                    const float *const *value_rows, size_t T, size_t n_heads, size_t n_kv_heads,
                    float scale, size_t threads, float *out);
+/* A prompt chunk as the reference's token-at-a-time loop runs it
+ * (crates/llm-gemma4/src/impl_/generate.rs:37-41, model.rs:407-410): query i
+ * (q + i*q_len, at position pos0 + i) attends rows [b, pos0 + i + 1) of the
+ * contiguous image keys/values (row t = position t), b = 0 when window == 0
+ * else windowed_len's start (eng/mod.rs:10-12); out + i*q_len receives it.
+ * Each query is or_attend; `threads` (>= 1) OS threads take queries in turn
+ * (a checker's parallelism, not the reference's).  status[i] (may be NULL)
+ * gets each query's result code; the call returns OR_ERR_COMPUTE if any
+ * query failed. */
+int or_attend_prefill(const float *q, size_t q_len, size_t N, const float *keys, const float *values,
+                      size_t pos0, size_t window, size_t n_heads, size_t n_kv_heads, float scale,
+                      size_t threads, int *status, float *out);
 /* f64 twin of attend: every product and sum in double, for the noise floor
  * |attend_f32 - attend_f64| that the tolerance policy falls back on. */
 int or_attend_f64(const float *q, size_t q_len, const float *keys, const float *values, size_t T,
@@ -74,10 +86,10 @@ int or_rope_heads(float *x, size_t len, size_t head_dim, size_t position, float 
                   const float *freq_factors, size_t n_factors);
 
 /* ---- policies: crates/llm-gemma4/src/idea/mod.rs, src/eng/mod.rs ---- */
-int or_layer_attention_kind(size_t n_layers, size_t layer);    /* idea/mod.rs:238-246: 0 local, 1 global */
+int or_layer_attention_kind(size_t n_layers, size_t layer);    /* idea/mod.rs:148-156: 0 local, 1 global */
 size_t or_head_dim(size_t n_layers, size_t layer, size_t head_dim_local,
-                   size_t head_dim_global);                     /* idea/mod.rs:230-235 */
-void or_proportional_rope_freq_factors(size_t head_dim, float p, float *out); /* idea/mod.rs:252-255 */
+                   size_t head_dim_global);                     /* idea/mod.rs:140-145 */
+void or_proportional_rope_freq_factors(size_t head_dim, float p, float *out); /* idea/mod.rs:162-165 */
 void or_windowed_len(size_t seq_len, size_t window, size_t *begin, size_t *end); /* eng/mod.rs:10-12 */
 int or_kv_source_layer(size_t n_layers, size_t shared_kv_layers, size_t layer,
                        size_t *source);                         /* eng/mod.rs:71-90 */
@@ -94,7 +106,7 @@ int or_kv_view(const or_kv_cache *c, size_t layer, size_t len, const float **key
                const float **values, size_t *width);                             /* :53-69 */
 void or_kv_clear(or_kv_cache *c);                                                /* :82-84 */
 
-/* Gemma4HyperParams fields the attention segment reads (idea/mod.rs:105-124). */
+/* Gemma4HyperParams fields the attention segment reads (idea/mod.rs:15-34). */
 typedef struct {
     size_t n_layers, n_heads, n_kv_heads, head_dim_local, head_dim_global;
     size_t sliding_window, shared_kv_layers;

@@ -64,6 +64,8 @@ def lib():
             "or_attend": (ctypes.c_int, [c_vp, c_size, c_vp, c_vp, c_size, c_size, c_size, c_f32, c_vp]),
             "or_attend_rows": (ctypes.c_int, [c_vp, c_size, c_vp, c_vp, c_size, c_size, c_size, c_f32, c_size,
                                               c_vp]),
+            "or_attend_prefill": (ctypes.c_int, [c_vp, c_size, c_size, c_vp, c_vp, c_size, c_size, c_size, c_size,
+                                                 c_f32, c_size, c_vp, c_vp]),
             "or_attend_f64": (ctypes.c_int, [c_vp, c_size, c_vp, c_vp, c_size, c_size, c_size, ctypes.c_double,
                                              c_vp]),
             "or_norm_heads": (ctypes.c_int, [c_vp, c_size, c_size, c_vp, c_f32]),
@@ -183,6 +185,25 @@ def attend_rows(q, keys, values, n_heads, n_kv_heads, scale=1.0, threads=0):
     _check(lib().or_attend_rows(q.ctypes.data, q.size, kr, vr, T, n_heads, n_kv_heads, scale, threads,
                                 out.ctypes.data))
     return out
+
+
+def attend_prefill(q, keys, values, pos0, window, n_heads, n_kv_heads, scale=1.0, threads=None):
+    """The token-at-a-time prompt loop (generate.rs:37-41): row i of q
+    [N, n_heads*head_dim] at position pos0 + i attends rows [b, pos0+i+1) of
+    the contiguous keys/values image (row t = position t; b from the window,
+    0 = global).  Returns (out [N, q_len], status [N]): status[i] is 0 or the
+    oracle's error code for that query; queries run on `threads` OS threads
+    (default: all CPUs)."""
+    q, keys, values = _f32(q), _f32(keys), _f32(values)
+    N, q_len = q.shape
+    if keys.shape[0] < pos0 + N or values.shape[0] < pos0 + N:
+        raise ValueError("keys/values must hold rows up to pos0 + N - 1")
+    threads = threads or os.cpu_count() or 1
+    out = np.zeros((N, q_len), dtype=np.float32)
+    status = np.zeros(N, dtype=np.int32)
+    lib().or_attend_prefill(q.ctypes.data, q_len, N, keys.ctypes.data, values.ctypes.data, pos0, window, n_heads,
+                            n_kv_heads, scale, threads, status.ctypes.data, out.ctypes.data)
+    return out, status
 
 
 class RowPointers:

@@ -107,6 +107,21 @@ def test_host_attend_mirror(ctx):
     assert I.rel_err(ctx.attend(q2, K2, V2, 4, 2, 1.0), orc.attend(q2, K2, V2, 4, 2)) <= TOL
 
 
+def test_host_attend_q_length_not_a_multiple_of_heads(ctx):
+    """head_dim = q.len() / n_heads; a q with a remainder leaves the heads'
+    concatenation shorter than q, and attend returns Compute("softmax input
+    is not finite") (model.rs:349, 362-364) -- the oracle and the backend."""
+    rng = np.random.default_rng(9)
+    d = 16
+    q = rng.standard_normal(8 * d + 3).astype(np.float32)
+    K = rng.standard_normal((5, d)).astype(np.float32)
+    V = rng.standard_normal((5, d)).astype(np.float32)
+    with pytest.raises(orc.OracleError, match="softmax input is not finite"):
+        orc.attend(q, K, V, 8, 1)
+    with pytest.raises(g4hip.EngError, match="softmax input is not finite"):
+        ctx.attend(q, K, V, 8, 1, 1.0)
+
+
 @pytest.mark.parametrize("d", [256, 512, 16])
 def test_non_finite_softmax_is_an_error(ctx, d):
     n_kv = 1

@@ -110,8 +110,8 @@ def _copy_out(ptr, n):
     return out
 
 
-@pytest.mark.parametrize("layer", [0, 4])
-def test_layer_attention_past_the_cache_fails_like_the_reference(ctx, layer):
+@pytest.mark.parametrize("layer,ring", [(0, False), (4, False), (0, True)])
+def test_layer_attention_past_the_cache_fails_like_the_reference(ctx, layer, ring):
     """model.rs:394-407 appends the new row, then views position + 1 rows: a
     position past the cached rows fails at the view with ContextTooLong and
     leaves the appended row in the cache.  The device cache must end in the
@@ -123,7 +123,7 @@ def test_layer_attention_past_the_cache_fails_like_the_reference(ctx, layer):
     d = 512 if layer == 4 else 256
     rng = np.random.default_rng(40 + layer)
     freqs = I.rope_freqs(7, 512)
-    cache = g4hip.KvCache(ctx, [256, 256, 256, 256, 512], 64)
+    cache = g4hip.KvCache(ctx, [256, 256, 256, 256, 512], 64, ring_rows=[24, 24, 24, 24, 0] if ring else None)
     ocache = orc.KvCache()
     try:
         hist = 3
@@ -163,3 +163,49 @@ def test_layer_attention_past_the_cache_fails_like_the_reference(ctx, layer):
         assert I.rel_err(host(out), ref) <= TOL
     finally:
         cache.close()
+
+
+def test_layer_attention_on_a_cache_longer_than_the_position(ctx):
+    """A cache that already holds more rows than the position: the append
+    pushes the new row after them (context_memory.rs:44-51) and the view
+    takes the first position + 1 rows (model.rs:405-407), so the step attends
+    cached rows only.  On a ring the new row and its mirror copy go to its
+    own slot: a later window that reads the row through the mirror must see
+    it.  Whole-history cache, ring cache and oracle agree."""
+    import g4hip
+    print("[case] layer_attention, cache longer than the position", flush=True)
+    hp_g = g4hip.G4Hparams(7, 8, 1, 256, 512, 16, 2, 10000.0, 1000000.0, 1e-6)
+    hp_o = orc.Hparams(7, 8, 1, 256, 512, 16, 2, 10000.0, 1000000.0, 1e-6)
+    d, layer, hist, R = 256, 0, 30, 24
+    rng = np.random.default_rng(77)
+    widths = [256, 256, 256, 256, 512]
+    full = g4hip.KvCache(ctx, widths, 64)
+    ringc = g4hip.KvCache(ctx, widths, 64, ring_rows=[R, R, R, R, 0])
+    ocache = orc.KvCache()
+    try:
+        K = rng.standard_normal((hist, d)).astype(np.float32)
+        V = rng.standard_normal((hist, d)).astype(np.float32)
+        for c in (full, ringc):
+            c.append_rows(layer, dev(K), dev(V), hist)
+        for t in range(hist):
+            ocache.append(layer, K[t], V[t])
+        wq, wk = (rng.uniform(0.5, 1.5, d).astype(np.float32) for _ in range(2))
+        # position 27 appends row 30 and attends rows [12, 28); position 31
+        # attends [16, 32), which holds row 30 -- on the ring, from its mirror.
+        for pos in (27, 31, 32):
+            q, k, v = (rng.standard_normal(m * d).astype(np.float32) for m in (8, 1, 1))
+            ref, src, rr, _, _, _ = ocache.layer_attention(hp_o, layer, pos, q, k, v, wq, wk, None)
+            outs = []
+            for c in (full, ringc):
+                out = torch.zeros(8 * d, device="cuda")
+                gsrc, grange = c.layer_attention(hp_g, layer, pos, dev(q), dev(k), dev(v), dev(wq), dev(wk), None, out)
+                ctx.check_status()
+                assert (gsrc, grange) == (src, rr), pos
+                outs.append(host(out))
+            print(f"[parity] position {pos}: rows {rr}, rel err {I.rel_err(outs[0], ref):.2e}", flush=True)
+            assert I.rel_err(outs[0], ref) <= TOL, pos
+            assert np.array_equal(outs[0], outs[1]), pos
+        assert full.len(layer) == ringc.len(layer) == hist + 3
+    finally:
+        full.close()
+        ringc.close()

@@ -195,3 +195,32 @@ def test_fused_quantization_entries_equal_the_two_step_calls(ctx, rows, cols):
             ctx.geglu_q8_0(gate, up, rows, cols, xs, xq, a, fp16_gelu=f16)
             ctx.gated_ffn_q8_0(gate, up, rows, cols, x, b, fp16_gelu=f16)
             assert torch.equal(a, b)
+
+
+def test_empty_rows(ctx):
+    """cols == 0: every output is the empty sum (the reference's -0.0, through
+    the soft-cap or the GELU gate), with no element read -- for the calls that
+    quantize the activation inside, and for the quantized-activation ones."""
+    rows = 5
+    e8 = np.zeros(0, np.uint8)
+    ef, ei = np.zeros(0, np.float32), np.zeros(0, np.int8)
+    w = torch.empty(0, dtype=torch.uint8, device="cuda")
+    x = torch.empty(0, device="cuda")
+    xs, xq = torch.empty(0, device="cuda"), torch.empty(0, dtype=torch.int8, device="cuda")
+    out = torch.full((rows,), 7.0, device="cuda")
+
+    def bits(t):
+        return host(t).view(np.uint32)
+
+    ref = orc.matvec_q8_0(e8, rows, 0, ef, ei).view(np.uint32)
+    ctx.project_q8_0(w, rows, 0, x, out)
+    assert np.array_equal(bits(out), ref)
+    ctx.matvec_q8_0(w, rows, 0, xs, xq, out)
+    assert np.array_equal(bits(out), ref)
+    ref = orc.matvec_q8_0(e8, rows, 0, ef, ei, softcap=30.0).view(np.uint32)
+    ctx.logits_q8_0(w, rows, 0, x, 30.0, out)
+    assert np.array_equal(bits(out), ref)
+    for f16 in (False, True):
+        ref = orc.geglu_q8_0(e8, e8, rows, 0, ef, ei, fp16_gelu=f16).view(np.uint32)
+        ctx.gated_ffn_q8_0(w, w, rows, 0, x, out, fp16_gelu=f16)
+        assert np.array_equal(bits(out), ref)
