@@ -163,6 +163,15 @@ int g4_init(int device, g4_ctx **out) {
             delete ctx;
             return g4::hip_failed(e, "g4_init");
         }
+        // This device's copy of the static decode scratch (with the device
+        // current): g4_attend_decode_noalloc passes this address, never the
+        // array's host-side name.
+        const int rc = g4::decode_scratch_address(&ctx->scratch, &ctx->scratch_bytes);
+        if (rc != G4_OK) {
+            (void)hipFree(ctx->status_dev);
+            delete ctx;
+            return rc;
+        }
         *out = ctx;
         return (int)G4_OK;
     });
@@ -212,33 +221,60 @@ static int check_heads(int n_heads, int n_kv_heads, int head_dim) {
     return G4_OK;
 }
 
+namespace {
+
+// g4_attend_decode, with the split partials in the context's workspace or,
+// when scratch is set, in the static scratch (no allocation).
+int attend_decode(g4_ctx *ctx, const float *q, const float *k_cache, const float *v_cache, int64_t row_stride,
+                  int64_t kv_begin, int64_t kv_end, int n_heads, int n_kv_heads, int head_dim, float scale,
+                  float *out, g4_stream stream, bool scratch) {
+    if (!ctx) return invalid("g4_attend_decode: null context");
+    int rc = check_heads(n_heads, n_kv_heads, head_dim);
+    if (rc != G4_OK) return rc;
+    if (row_stride < (int64_t)n_kv_heads * head_dim) return invalid("row_stride below the row width");
+    if (kv_begin < 0 || kv_end <= kv_begin)
+        return g4::set_error(G4_ERR_COMPUTE, "softmax input is not finite");
+    g4::DecodeArgs a{};
+    a.B = 1;
+    a.q = q;
+    a.k = k_cache;
+    a.v = v_cache;
+    a.row_stride = row_stride;
+    a.kv_begin0 = kv_begin;
+    a.kv_end0 = kv_end;
+    a.max_kv_len = kv_end - kv_begin;
+    a.prefill_window = -1;
+    a.n_heads = n_heads;
+    a.n_kv_heads = n_kv_heads;
+    a.head_dim = head_dim;
+    a.scale = scale;
+    a.out = out;
+    if (scratch) {
+        a.scratch = ctx->scratch;
+        a.scratch_bytes = ctx->scratch_bytes;
+    }
+    return g4::launch_decode(ctx, a, as_stream(stream));
+}
+
+}  // namespace
+
 int g4_attend_decode(g4_ctx *ctx, const float *q, const float *k_cache, const float *v_cache,
                      int64_t row_stride, int64_t kv_begin, int64_t kv_end, int n_heads,
                      int n_kv_heads, int head_dim, float scale, float *out, g4_stream stream) {
     return guarded([&] {
         g4::clear_error();
-        if (!ctx) return invalid("g4_attend_decode: null context");
-        int rc = check_heads(n_heads, n_kv_heads, head_dim);
-        if (rc != G4_OK) return rc;
-        if (row_stride < (int64_t)n_kv_heads * head_dim) return invalid("row_stride below the row width");
-        if (kv_begin < 0 || kv_end <= kv_begin)
-            return g4::set_error(G4_ERR_COMPUTE, "softmax input is not finite");
-        g4::DecodeArgs a{};
-        a.B = 1;
-        a.q = q;
-        a.k = k_cache;
-        a.v = v_cache;
-        a.row_stride = row_stride;
-        a.kv_begin0 = kv_begin;
-        a.kv_end0 = kv_end;
-        a.max_kv_len = kv_end - kv_begin;
-        a.prefill_window = -1;
-        a.n_heads = n_heads;
-        a.n_kv_heads = n_kv_heads;
-        a.head_dim = head_dim;
-        a.scale = scale;
-        a.out = out;
-        return g4::launch_decode(ctx, a, as_stream(stream));
+        return attend_decode(ctx, q, k_cache, v_cache, row_stride, kv_begin, kv_end, n_heads, n_kv_heads, head_dim,
+                             scale, out, stream, false);
+    });
+}
+
+int g4_attend_decode_noalloc(g4_ctx *ctx, const float *q, const float *k_cache, const float *v_cache,
+                             int64_t row_stride, int64_t kv_begin, int64_t kv_end, int n_heads, int n_kv_heads,
+                             int head_dim, float scale, float *out, g4_stream stream) {
+    return guarded([&] {
+        g4::clear_error();
+        return attend_decode(ctx, q, k_cache, v_cache, row_stride, kv_begin, kv_end, n_heads, n_kv_heads, head_dim,
+                             scale, out, stream, true);
     });
 }
 

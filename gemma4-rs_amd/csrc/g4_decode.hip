@@ -1068,11 +1068,20 @@ int launch_mode(g4_ctx *ctx, const DecodeArgs &a, DecodeK p, hipStream_t stream,
     if (max_splits > 1) {
         const size_t slots = (size_t)units * max_splits * group;
         const size_t bytes = slots * D * sizeof(float) + slots * sizeof(float2) + 256;
-        int rc = ensure_workspace(ctx, bytes, stream);
-        if (rc != G4_OK) return rc;
-        p.part_o = (float *)ctx->ws.ptr;
+        void *ws = a.scratch;
+        if (ws) {
+            if (bytes > a.scratch_bytes)
+                return set_error(G4_ERR_COMPUTE, "g4_attend_decode_noalloc: this decode needs " + std::to_string(bytes) +
+                                                     " bytes of split scratch, above the static " +
+                                                     std::to_string(a.scratch_bytes));
+        } else {
+            int rc = ensure_workspace(ctx, bytes, stream);
+            if (rc != G4_OK) return rc;
+            ws = ctx->ws.ptr;
+        }
+        p.part_o = (float *)ws;
         size_t off = (slots * D * sizeof(float) + 255) / 256 * 256;
-        p.part_ml = (float2 *)((char *)ctx->ws.ptr + off);
+        p.part_ml = (float2 *)((char *)ws + off);
     }
     dim3 grid((unsigned)max_splits, (unsigned)a.n_kv_heads, (unsigned)a.B);
     const bool stream_kv = MODE == kSingle && max_splits > 1;  // K/V read once per step: NT loads
@@ -1120,8 +1129,28 @@ int launch_mode(g4_ctx *ctx, const DecodeArgs &a, DecodeK p, hipStream_t stream,
 
 }  // namespace
 
+// Split partials of g4_attend_decode_noalloc, for callers that cannot
+// allocate.  One array per GPU, shared by every such call on it (calls that
+// overlap on one GPU race).  8 MiB + 64 KiB holds the partials of any split
+// plan with one KV head (at most kMaxSplits splits of 8 heads x 512 floats,
+// plus their (m, l) pairs).  Nothing in it needs to start at zero: each split
+// writes its partial before the merge reads it.
+constexpr size_t kDecodeScratchBytes = (8u << 20) + (64u << 10);
+static __device__ __align__(256) unsigned char scratch[kDecodeScratchBytes];
+
+int decode_scratch_address(void **ptr, size_t *bytes) {
+    void *p = nullptr;
+    G4_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) return set_error(G4_ERR_COMPUTE, "hip: no device address for the decode scratch");
+    *ptr = p;
+    *bytes = kDecodeScratchBytes;
+    return G4_OK;
+}
+
 int launch_decode(g4_ctx *ctx, const DecodeArgs &a, hipStream_t stream) {
     if (a.B <= 0) return G4_OK;
+    if (a.scratch && (a.B != 1 || a.kv_begin || a.prefill_window >= 0))
+        return set_error(G4_ERR_COMPUTE, "decode scratch: single-sequence decodes only");
     DecodeK p{};
     p.q = a.q;
     p.k = a.k;

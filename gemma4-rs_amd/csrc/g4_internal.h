@@ -46,6 +46,8 @@ struct g4_ctx {
     int64_t *zero_rows = nullptr;    // device zeros: default row offsets of a batch
     int64_t zero_rows_len = 0;
     void *prefill_plan = nullptr;    // work-unit table of the last prefill shape
+    void *scratch = nullptr;         // this device's static decode scratch (g4_attend_decode_noalloc)
+    size_t scratch_bytes = 0;
 };
 
 namespace g4 {
@@ -76,8 +78,16 @@ struct DecodeArgs {
     int n_heads, n_kv_heads, head_dim;
     float scale;
     float *out;
+    // When set, the split partials go here instead of the context's
+    // workspace (nothing is allocated); a shape that needs more than
+    // scratch_bytes is refused.  Single-sequence decodes only.
+    void *scratch;
+    size_t scratch_bytes;
 };
 int launch_decode(g4_ctx *ctx, const DecodeArgs &a, hipStream_t stream);
+// The device address (on the current device) and size of the static scratch
+// array that g4_attend_decode_noalloc uses.
+int decode_scratch_address(void **ptr, size_t *bytes);
 
 // A layer's decode step with its input preparation fused in (the layer
 // driver's form): the decode kernel prepares q itself (rms_norm with q_w,

@@ -58,6 +58,8 @@ _SIGS = {
     "g4_set_decode_chunk": (c_int, [c_vp, c_i64]),
     "g4_attend": (c_int, [c_vp, c_vp, c_size, c_vp, c_vp, c_size, c_size, c_size, c_f32, c_vp]),
     "g4_attend_decode": (c_int, [c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_int, c_int, c_int, c_f32, c_vp, c_vp]),
+    "g4_attend_decode_noalloc": (c_int, [c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_int, c_int, c_int, c_f32, c_vp,
+                                         c_vp]),
     "g4_attend_decode_batch": (c_int, [c_vp, c_int, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_int, c_int,
                                        c_int, c_f32, c_vp, c_vp]),
     "g4_attend_prefill": (c_int, [c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_int, c_int, c_int, c_f32,
@@ -253,6 +255,14 @@ class Context:
         stride = row_stride if row_stride is not None else n_kv_heads * head_dim
         _raise(lib().g4_attend_decode(self.handle, _ptr(q), _ptr(k_cache), _ptr(v_cache), stride, kv_begin,
                                       kv_end, n_heads, n_kv_heads, head_dim, scale, _ptr(out), _stream(stream)))
+
+    def attend_decode_noalloc(self, q, k_cache, v_cache, kv_begin, kv_end, n_heads, n_kv_heads, head_dim,
+                              out, scale=1.0, row_stride=None, stream=None):
+        """g4_attend_decode with its split partials in the static scratch (no allocation)."""
+        stride = row_stride if row_stride is not None else n_kv_heads * head_dim
+        _raise(lib().g4_attend_decode_noalloc(self.handle, _ptr(q), _ptr(k_cache), _ptr(v_cache), stride, kv_begin,
+                                              kv_end, n_heads, n_kv_heads, head_dim, scale, _ptr(out),
+                                              _stream(stream)))
 
     def attend_decode_batch(self, q, k_base, v_base, seq_row0, kv_begin, kv_end, max_kv_len, n_heads,
                             n_kv_heads, head_dim, out, scale=1.0, row_stride=None, stream=None):

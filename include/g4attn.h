@@ -82,6 +82,21 @@ int g4_attend_decode(g4_ctx *ctx, const float *q_dev, const float *k_cache_dev,
                      int64_t kv_end, int n_heads, int n_kv_heads, int head_dim, float scale,
                      float *out_dev, g4_stream stream);
 
+/* g4_attend_decode that allocates nothing.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  The split
+ * partials go to a static device array of 8 MiB + 64 KiB, one per GPU, whose
+ * address g4_init resolves; a decode whose split plan needs more is refused
+ * with G4_ERR_COMPUTE (any range with one KV head and 8 query heads fits).
+ * Same arguments, results and stream semantics as g4_attend_decode.  Every
+ * call on a GPU shares that GPU's array: calls that overlap in time on one
+ * GPU (other streams, other contexts) race and must be serialised by the
+ * caller. */
+int g4_attend_decode_noalloc(g4_ctx *ctx, const float *q_dev, const float *k_cache_dev,
+                             const float *v_cache_dev, int64_t row_stride, int64_t kv_begin,
+                             int64_t kv_end, int n_heads, int n_kv_heads, int head_dim, float scale,
+                             float *out_dev, g4_stream stream);
+
 /* B independent decode steps in one launch (ragged lengths).  Sequence s
  * reads rows [kv_begin[s], kv_end[s]) of its cache, whose row 0 is row
  * seq_row0[s] of k_base/v_base (seq_row0 may be NULL: all zero).  The three
