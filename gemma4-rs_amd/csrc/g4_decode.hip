@@ -222,14 +222,25 @@ constexpr int kBufferWord3 = 0x00020000;
 // Cache-policy operand of a buffer store: SC1, device scope -- the store is
 // written through the XCD's L2 to the point of coherence.
 constexpr int kDeviceScope = 16;
-// Cache-policy operand of a buffer load: NT, non-temporal (streamed, not kept
-// for reuse).  A single sequence split over many workgroups reads K/V with it
-// (4096 keys from HBM: 11.23 -> 10.93 us; 512 keys: 8.12 -> 7.59 us): its
-// rows are read once per step.  Batches, unsplit sequences and the ragged
-// stream kernel read with the default policy: when their rows are still
-// cached from the previous step, NT loads were slower (a 32-sequence sliding
-// batch 21.1 -> 23.1 us, 64 keys 6.75 -> 6.88 us, the stream kernel 4%).
+// Cache-policy operand of a buffer load: NT, non-temporal (streamed, not
+// kept for reuse).
 constexpr int kNonTemporal = 2;
+// The cache policies of a decode's K and V loads, packed into one template
+// argument: K's operand in the low byte, V's in the next.  A K load covers
+// half of each 128-byte line it touches (4 lanes x 16 bytes of a key), the
+// other half following in the next load; a V load covers whole lines.  With
+// NT loads on K the first half's line is not kept for the second, while NT
+// on V alone streams faster in every form measured (event-timed graph
+// replays, against NT on both or on neither):
+//   ragged batch, 32 global sequences (2 GB):    345 -> 318 us (6.4 TB/s)
+//   one sequence, 4096 keys d=512 (HBM-cold):   10.1 -> 9.5 us
+//   one sequence, 8192 keys d=512:              12.2 -> 11.0 us
+//   ragged batch, 32 sliding windows of 512:    12.9 -> 12.5 us
+// K keeps the default policy; NT on K was slower (351 us on the first).
+constexpr int kv_policy(int k, int v) { return k | (v << 8); }
+constexpr int kPolicyK(int aux) { return aux & 0xff; }
+constexpr int kPolicyV(int aux) { return (aux >> 8) & 0xff; }
+constexpr int kKvPolicy = kv_policy(0, kNonTemporal);
 
 // A wavefront's view of one (sequence, KV head) decode: lane (g, c) =
 // (lane/16, lane%16) of wave w, which owns head dims [base, base + DW).
@@ -278,13 +289,14 @@ struct DecodeLane {
         const uint32_t toff = (uint32_t)tile * tile_bytes;
 #pragma unroll
         for (int u = 0; u < KU; ++u)
-            T.k[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, koff + toff + 64u * u, 0, AUX));
+            T.k[u] = __builtin_bit_cast(
+                f32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, koff + toff + 64u * u, 0, kPolicyK(AUX)));
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             if constexpr (TW == 4)
-                T.v[r] = __builtin_bit_cast(VRow, __builtin_amdgcn_raw_buffer_load_b128(vrs, voff[r] + toff, 0, AUX));
+                T.v[r] = __builtin_bit_cast(VRow, __builtin_amdgcn_raw_buffer_load_b128(vrs, voff[r] + toff, 0, kPolicyV(AUX)));
             else
-                T.v[r] = __builtin_bit_cast(VRow, __builtin_amdgcn_raw_buffer_load_b64(vrs, voff[r] + toff, 0, AUX));
+                T.v[r] = __builtin_bit_cast(VRow, __builtin_amdgcn_raw_buffer_load_b64(vrs, voff[r] + toff, 0, kPolicyV(AUX)));
         }
     }
 };
@@ -330,8 +342,9 @@ struct DecodeAcc {
     // the LDS round trip, the softmax's dependent steps -- is paid once per
     // 32 keys.  NT = 1: only the first tile (a split of at most 16 keys).
     template <int NT = 2>
-    __device__ __forceinline__ void pair(const L &ln, const KvTile<D> (&P)[2], int valid, float scale,
-                                         PairScores<D> &sx, int &buf) {
+    __device__ __forceinline__ void pair(const L &ln, const KvTile<D> &P0, const KvTile<D> &P1, int valid,
+                                         float scale, PairScores<D> &sx, int &buf) {
+        const KvTile<D> *P[2] = {&P0, &P1};
         // Partial S^T of both tiles over this wave's dims (two MFMA chains).
         f32x4 acc[2] = {};
 #pragma unroll
@@ -340,7 +353,7 @@ struct DecodeAcc {
             for (int j = 0; j < 4; ++j)
 #pragma unroll
                 for (int t = 0; t < NT; ++t)
-                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(P[t].k[u][j], qreg[u][j], acc[t], 0, 0, 0);
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(P[t]->k[u][j], qreg[u][j], acc[t], 0, 0, 0);
 
         // The tiles' S^T: the waves' partials summed in a fixed order, so
         // every wave holds the same bits (all reads issue before the first add).
@@ -401,7 +414,7 @@ struct DecodeAcc {
             for (int r = 0; r < 4; ++r)
 #pragma unroll
                 for (int i = 0; i < TW; ++i)
-                    o[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(P[t].v[r][i], pr[4 * t + r], o[i], 0, 0, 0);
+                    o[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(P[t]->v[r][i], pr[4 * t + r], o[i], 0, 0, 0);
     }
 
     // One more key whose value row is held in LDS (vrow, D floats): sv is its
@@ -504,13 +517,13 @@ struct PairPipe {
 #pragma unroll
             for (int b = 0; b < NPAIR; ++b) {
                 load_pair(ln, krs, vrs, q_first, n_pairs, i0 + b + NPAIR - 1, T[(b + NPAIR - 1) % NPAIR]);
-                acc.pair(ln, T[b], n_keys - 32 * (q_first + i0 + b), scale, sx, buf);
+                acc.pair(ln, T[b][0], T[b][1], n_keys - 32 * (q_first + i0 + b), scale, sx, buf);
             }
         }
         // Tail: the remaining (< NPAIR) pairs are already buffered in T[0..].
 #pragma unroll
         for (int b = 0; b < NPAIR - 1; ++b)
-            if (i0 + b < n_pairs) acc.pair(ln, T[b], n_keys - 32 * (q_first + i0 + b), scale, sx, buf);
+            if (i0 + b < n_pairs) acc.pair(ln, T[b][0], T[b][1], n_keys - 32 * (q_first + i0 + b), scale, sx, buf);
     }
 };
 
@@ -524,7 +537,7 @@ __device__ __forceinline__ void run_pairs(const DecodeLane<D> &ln, DecodeAcc<D> 
         // loads after it, so the scores overlap the V transfer; issuing all
         // eight loads at once measured slower (4096 keys: 10.3 -> 11.2 us).
         ln.template load_tile<AUX>(krs, vrs, 2 * q_first, pp.T[0][0]);
-        acc.template pair<1>(ln, pp.T[0], n_keys - 32 * q_first, scale, sx, buf);
+        acc.template pair<1>(ln, pp.T[0][0], pp.T[0][0], n_keys - 32 * q_first, scale, sx, buf);
         return;
     }
     pp.prime(ln, krs, vrs, q_first, n_pairs);
@@ -653,7 +666,7 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::NW) void decode_layer_kernel(D
     int buf = 0;
     if (n_keys > 0) {
         if (single)
-            acc.template pair<1>(ln, pp.T[0], n_keys, p.scale, sx, buf);
+            acc.template pair<1>(ln, pp.T[0][0], pp.T[0][0], n_keys, p.scale, sx, buf);
         else
             pp.finish(ln, acc, krs, vrs, 0, n_pairs, n_keys, p.scale, sx, buf);
     }
@@ -770,7 +783,7 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::NW) void decode_stream_kernel(
         const __amdgpu_buffer_rsrc_t krs = ln.rows(p.k + first, n_keys, stride);
         const __amdgpu_buffer_rsrc_t vrs = ln.rows(p.v + first, n_keys, stride);
         acc.start(ln, p.q + ((int64_t)cs * p.n_heads + head) * D);
-        run_pairs<D, NBUF, 0>(ln, acc, krs, vrs, g - ga, ge - g, n_keys, p.scale, sx, buf);
+        run_pairs<D, NBUF, kKvPolicy>(ln, acc, krs, vrs, g - ga, ge - g, n_keys, p.scale, sx, buf);
         if (g == ga && ge == gb) {
             acc.write_output(ln, p.out + ((int64_t)cs * p.n_heads + head) * D, col_valid, p.status);
         } else {  // slot 0: the run's first sequence; 1: its last
@@ -1084,37 +1097,19 @@ int launch_mode(g4_ctx *ctx, const DecodeArgs &a, DecodeK p, hipStream_t stream,
         p.part_ml = (float2 *)((char *)ws + off);
     }
     dim3 grid((unsigned)max_splits, (unsigned)a.n_kv_heads, (unsigned)a.B);
-    const bool stream_kv = MODE == kSingle && max_splits > 1;  // K/V read once per step: NT loads
     if (MODE == kSingle && lp) {
-        if (D == 256) {
-            if (stream_kv)
-                hipLaunchKernelGGL((decode_layer_kernel<256, kDecodeBuffers, kNonTemporal>), grid,
-                                   dim3(64 * DecodeShape<256>::NW), 0, stream, p, *lp);
-            else
-                hipLaunchKernelGGL((decode_layer_kernel<256, kDecodeBuffers, 0>), grid,
-                                   dim3(64 * DecodeShape<256>::NW), 0, stream, p, *lp);
-        } else {
-            if (stream_kv)
-                hipLaunchKernelGGL((decode_layer_kernel<512, kDecodeBuffers, kNonTemporal>), grid,
-                                   dim3(64 * DecodeShape<512>::NW), 0, stream, p, *lp);
-            else
-                hipLaunchKernelGGL((decode_layer_kernel<512, kDecodeBuffers, 0>), grid,
-                                   dim3(64 * DecodeShape<512>::NW), 0, stream, p, *lp);
-        }
+        if (D == 256)
+            hipLaunchKernelGGL((decode_layer_kernel<256, kDecodeBuffers, kKvPolicy>), grid,
+                               dim3(64 * DecodeShape<256>::NW), 0, stream, p, *lp);
+        else
+            hipLaunchKernelGGL((decode_layer_kernel<512, kDecodeBuffers, kKvPolicy>), grid,
+                               dim3(64 * DecodeShape<512>::NW), 0, stream, p, *lp);
     } else if (D == 256) {
-        if (stream_kv)
-            hipLaunchKernelGGL((decode_split_kernel<256, MODE, kDecodeBuffers, kNonTemporal>), grid,
-                               dim3(64 * DecodeShape<256>::NW), 0, stream, p);
-        else
-            hipLaunchKernelGGL((decode_split_kernel<256, MODE, kDecodeBuffers, 0>), grid,
-                               dim3(64 * DecodeShape<256>::NW), 0, stream, p);
+        hipLaunchKernelGGL((decode_split_kernel<256, MODE, kDecodeBuffers, kKvPolicy>), grid,
+                           dim3(64 * DecodeShape<256>::NW), 0, stream, p);
     } else {
-        if (stream_kv)
-            hipLaunchKernelGGL((decode_split_kernel<512, MODE, kDecodeBuffers, kNonTemporal>), grid,
-                               dim3(64 * DecodeShape<512>::NW), 0, stream, p);
-        else
-            hipLaunchKernelGGL((decode_split_kernel<512, MODE, kDecodeBuffers, 0>), grid,
-                               dim3(64 * DecodeShape<512>::NW), 0, stream, p);
+        hipLaunchKernelGGL((decode_split_kernel<512, MODE, kDecodeBuffers, kKvPolicy>), grid,
+                           dim3(64 * DecodeShape<512>::NW), 0, stream, p);
     }
     G4_HIP(hipGetLastError());
     if (max_splits > 1) {
