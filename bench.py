@@ -1,25 +1,33 @@
 """Benchmark of the MI355X attention backend for gemma4-rs.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME]
 
-A step is one global-layer decode-attention call (Gemma 4 E2B shape: 8 query
-heads sharing 1 KV head, head_dim 512, proportional NEOX RoPE, context 4096,
-query at position 4095), on f32 inputs already resident in HBM.  Each step
-reads a different copy of the K/V cache from a pool larger than the 256 MB
-Infinity Cache, so every step streams its K/V from HBM.
+Every decode and prefill shape of the five benchmark configurations runs on
+f32 inputs already resident in HBM; the timed steps are replays of captured
+HIP graphs, timed with HIP events on the stream the kernels run on.
 
-Printed: one JSON line.  `value` is the achieved HBM bandwidth of the step in
-GB/s (algorithmic bytes: the K and V rows attended, q and the output, each
-once); `ms_per_step` is the wall time per step; `roofline` relates the decode
-kernels' time to MI355X's 8 TB/s; `cpu_baseline` is the oracle (the C
-restatement of the reference's CPU attention, same `concat` copy and per-head
-thread pool) timed on this host's cores on a bounded sample of the same step.
-`workloads` carries the other measured shapes (sliding decode, the 35-layer
-stack, 2048-token prefill, the ragged 32-sequence batch, the layer drivers with
-their fused input preparation, the Q8_0 mat-vecs of the output head and a
-projection).
+The headline step is the largest configuration: a ragged batch of 32
+independent sequences (context lengths U[1024, 32768], seed 2024), one
+decode token each, through a global layer (head_dim 512, whole contexts,
+2.04 GB of K/V) and a sliding layer (head_dim 256, window 512), one launch
+per layer.  `value` is the step's achieved HBM bandwidth in GB/s
+(algorithmic bytes: the K and V rows attended, q and the output, each once);
+`roofline` relates the global layer's launch -- the dominant kernel -- to
+MI355X's 8 TB/s; `cpu_baseline` is the oracle (the C restatement of the
+reference's CPU attention with its `concat` copy and per-head thread pool)
+running the reference's per-sequence loop on this host's cores.
+
+`configs` carries each of the five configurations with its own roofline and
+CPU baseline: 1 sliding decode over 64 keys, 2 global decode over 4096 keys
+(HBM-cold: K/V copies rotated), 3 the 35-layer E2B stack at context 8192
+(cold and resident), 4 a 2048-token prefill through a sliding and a global
+layer (MFMA-bound), 5 the ragged batch.  `workloads` adds the layer drivers
+with their fused input preparation, the Q8_0 mat-vecs and the launch and
+streaming-read floors.  HBM byte counters come from the committed rocprofv3
+summaries under profiles/.
 """
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -37,6 +45,8 @@ EPS = 1e-6
 LOCAL_BASE, GLOBAL_BASE = 10000.0, 1000000.0
 WINDOW = 512
 MALL_BYTES = 256 << 20
+RAGGED_SEED, RAGGED_B = 2024, 32
+METRIC = "decode-attn µs/layer + achieved HBM GB/s; prefill-attn TFLOP/s (1× MI355X)"
 
 
 def decode_bytes(rows, d):
@@ -48,6 +58,19 @@ def prefill_flops(N, window, d):
     """4 * heads * d FLOP per attended (query, key) pair (QK^T and PV)."""
     pairs = sum(min(i + 1, window) if window else i + 1 for i in range(N))
     return 4 * N_HEADS * d * pairs
+
+
+def roofline_hbm(nbytes, seconds, traffic=None, **extra):
+    gbs = nbytes / seconds / 1e9
+    r = {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic}
+    r.update(extra)
+    return r
+
+
+def ragged_lengths():
+    import numpy as np
+    return np.random.default_rng(RAGGED_SEED).integers(1024, 32768 + 1, size=RAGGED_B).astype(np.int64)
 
 
 class Prep:
@@ -73,36 +96,52 @@ class Prep:
         return self.torch.rand(d // 2, device="cuda", generator=self.gen) * 7.0 + 1.0
 
 
-def time_steps(torch, fn, steps, warmup, block=1):
-    """Runs `warmup` eager steps, captures steps 0..block-1 into one HIP graph,
-    then times exactly `steps` steps (whole graph replays, the remainder
-    eagerly) between synchronisations.  fn(i) launches step i on the current
-    stream.  Returns (wall seconds, event seconds) for the timed steps."""
+def time_steps(torch, fn, steps, warmup):
+    """Runs `warmup` eager steps, captures the `steps` timed steps into one
+    HIP graph and times one replay of it between synchronisations, with HIP
+    events on the current stream (where fn(i) launches step i) and with the
+    host clock.  Returns (wall seconds, event seconds) for the `steps`
+    steps."""
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        for i in range(block):
+        for i in range(steps):
             fn(i)
     torch.cuda.synchronize()
-    graph.replay()  # first replay uploads the graph
+    graph.replay()  # the first replay uploads the graph
     torch.cuda.synchronize()
-    replays, rest = divmod(steps, block)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     start.record()
-    for _ in range(replays):
-        graph.replay()
-    for i in range(rest):
-        fn(i)
+    graph.replay()
     end.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     return wall, start.elapsed_time(end) * 1e-3
 
 
+# ----------------------------------------------------------------- GPU side
+def bench_sliding_decode(ctx, torch, prep, steps, warmup, T=64, d=256):
+    """Configuration 1: one sliding-layer decode over 64 keys (147 KB; its
+    rows stay cached between steps: a launch-latency figure)."""
+    K = prep.rows(T, d, 0, LOCAL_BASE, None)
+    V = prep.rows(T, d, 0, 0.0, None, rope=False)
+    q = prep.rows(1, d, T - 1, LOCAL_BASE, None, heads=N_HEADS)
+    out = torch.zeros(N_HEADS * d, device="cuda")
+    wall, ev = time_steps(torch, lambda i: ctx.attend_decode(q, K, V, 0, T, N_HEADS, N_KV, d, out), steps, warmup)
+    ctx.check_status()
+    host = {"q": q.cpu().numpy(), "K": K.cpu().numpy(), "V": V.cpu().numpy()}
+    return {"us_per_layer": ev / steps * 1e6, "wall_us_per_layer": wall / steps * 1e6, "bytes": decode_bytes(T, d),
+            "cache": "resident (147 KB, read every step)", "host": host}
+
+
 def bench_global_decode(ctx, torch, prep, steps, warmup, T=4096, d=512):
+    """Configuration 2: one global-layer decode over 4096 keys.  Each step
+    reads one of `copies` K/V copies (more than 1.5x the 256 MB Infinity
+    Cache between two reads of a copy), so its K/V come from HBM; the same
+    step on one resident copy is reported beside it."""
     freqs = prep.rope_freqs(d)
     per_copy = 2 * T * d * 4
     copies = max(2, int(1.5 * MALL_BYTES // per_copy) + 1)
@@ -117,70 +156,81 @@ def bench_global_decode(ctx, torch, prep, steps, warmup, T=4096, d=512):
         c = i % copies
         ctx.attend_decode(q, Ks[c], Vs[c], 0, T, N_HEADS, N_KV, d, out)
 
-    wall, ev = time_steps(torch, step, steps, warmup, block=copies)
+    wall, ev = time_steps(torch, step, steps, warmup)
     ctx.check_status()
-    # the same step with one resident copy (served from the Infinity Cache)
     wall_w, ev_w = time_steps(torch, lambda i: ctx.attend_decode(q, Ks[0], Vs[0], 0, T, N_HEADS, N_KV, d, out),
-                              steps, warmup, block=copies)
+                              steps, warmup)
     host = {"q": q.cpu().numpy(), "K": Ks[0].cpu().numpy(), "V": Vs[0].cpu().numpy()}
-    return {"wall": wall, "event": ev, "wall_warm": wall_w, "event_warm": ev_w, "copies": copies,
-            "bytes": decode_bytes(T, d), "host": host}
-
-
-def bench_sliding_decode(ctx, torch, prep, steps, warmup, T=64, d=256):
-    K = prep.rows(T, d, 0, LOCAL_BASE, None)
-    V = prep.rows(T, d, 0, 0.0, None, rope=False)
-    q = prep.rows(1, d, T - 1, LOCAL_BASE, None, heads=N_HEADS)
-    out = torch.zeros(N_HEADS * d, device="cuda")
-    wall, ev = time_steps(torch, lambda i: ctx.attend_decode(q, K, V, 0, T, N_HEADS, N_KV, d, out), steps, warmup,
-                          block=20)
-    ctx.check_status()
     return {"us_per_layer": ev / steps * 1e6, "wall_us_per_layer": wall / steps * 1e6,
-            "bytes": decode_bytes(T, d)}
+            "us_per_layer_resident": ev_w / steps * 1e6, "bytes": decode_bytes(T, d),
+            "cache": f"HBM-cold: {min(copies, steps)} K/V copies of {per_copy >> 20} MiB rotated", "host": host}
 
 
-def bench_stack(ctx, torch, prep, g4hip, steps, warmup, ctx_len=8192):
-    """35-layer E2B stack, one decode step at position ctx_len-1: each layer's
-    attention over its source layer's cache (owners 0..14, shared 15..34)."""
+def stack_plan(g4hip, ctx_len):
+    """The E2B stack's per-layer (source layer, kv range, head_dim, global)."""
     n_layers, shared = 35, 20
-    freqs = prep.rope_freqs(512)
-    caches = {}
     plan = []
-    total_bytes = 0
     for layer in range(n_layers):
         glob = g4hip.layer_attention_kind(n_layers, layer) == "global"
         d = 512 if glob else 256
         src = g4hip.kv_source_layer(n_layers, shared, layer)
-        if src == layer:
-            caches[layer] = (prep.rows(ctx_len, d, 0, GLOBAL_BASE if glob else LOCAL_BASE, freqs if glob else None),
-                             prep.rows(ctx_len, d, 0, 0.0, None, rope=False))
         r = g4hip.windowed_len(ctx_len, WINDOW) if not glob else range(0, ctx_len)
-        q = prep.rows(1, d, ctx_len - 1, GLOBAL_BASE if glob else LOCAL_BASE, freqs if glob else None,
-                      heads=N_HEADS)
-        plan.append((src, r.start, r.stop, d, q, torch.zeros(N_HEADS * d, device="cuda")))
-        total_bytes += decode_bytes(r.stop - r.start, d)
+        plan.append((layer, src, r.start, r.stop, d, glob))
+    return plan
+
+
+def bench_stack(ctx, torch, prep, g4hip, steps, warmup, ctx_len=8192, cold=True, want_host=False):
+    """Configuration 3: the 35-layer E2B stack, one decode step at position
+    ctx_len - 1: each layer's attention over its source layer's cache
+    (owners 0..14, layers 15..34 reading 13/14), one call per layer.  Cold:
+    the 15 owners' caches exist in `copies` copies, one per step in turn, so
+    the 108 MiB of K/V one step reads come from HBM; resident: one copy."""
+    plan = stack_plan(g4hip, ctx_len)
+    freqs = prep.rope_freqs(512)
+    unique = sum(decode_bytes(e - b, d) for (l, s, b, e, d, g) in plan if s == l)
+    copies = max(2, int(1.5 * MALL_BYTES // unique) + 1) if cold else 1
+    caches = []
+    for c in range(copies):
+        caches.append({})
+        for layer, src, b, e, d, glob in plan:
+            if src == layer:
+                caches[c][layer] = (prep.rows(ctx_len, d, 0, GLOBAL_BASE if glob else LOCAL_BASE,
+                                              freqs if glob else None),
+                                    prep.rows(ctx_len, d, 0, 0.0, None, rope=False))
+    qs = [prep.rows(1, d, ctx_len - 1, GLOBAL_BASE if glob else LOCAL_BASE, freqs if glob else None, heads=N_HEADS)
+          for (layer, src, b, e, d, glob) in plan]
+    outs = [torch.zeros(N_HEADS * d, device="cuda") for (layer, src, b, e, d, glob) in plan]
+    total_bytes = sum(decode_bytes(e - b, d) for (l, s, b, e, d, g) in plan)
 
     def step(i):
-        for src, b, e, d, q, out in plan:
-            K, V = caches[src]
+        cc = caches[i % copies]
+        for (layer, src, b, e, d, glob), q, out in zip(plan, qs, outs):
+            K, V = cc[src]
             ctx.attend_decode(q, K, V, b, e, N_HEADS, N_KV, d, out)
 
     wall, ev = time_steps(torch, step, steps, warmup)
     ctx.check_status()
-    n_glob = sum(1 for p in plan if p[3] == 512)
-    return {"us_per_stack": ev / steps * 1e6, "wall_us_per_stack": wall / steps * 1e6,
-            "us_per_layer_mean": ev / steps / n_layers * 1e6, "bytes_per_stack": total_bytes,
-            "gbs": total_bytes / (ev / steps) / 1e9, "layers": n_layers, "global_layers": n_glob}
+    res = {"us_per_stack": ev / steps * 1e6, "wall_us_per_stack": wall / steps * 1e6,
+           "us_per_layer_mean": ev / steps / len(plan) * 1e6, "bytes_per_stack": total_bytes,
+           "unique_bytes_per_stack": unique, "layers": len(plan),
+           "global_layers": sum(1 for p in plan if p[5]),
+           "cache": (f"HBM-cold: {min(copies, steps)} copies of the owners' K/V rotated" if cold else
+                     "resident: one copy, re-read every step")}
+    if want_host:
+        res["host"] = {"plan": plan, "q": [q.cpu().numpy() for q in qs],
+                       "kv": {l: (K.cpu().numpy(), V.cpu().numpy()) for l, (K, V) in caches[0].items()}}
+    return res
 
 
-def bench_prefill(ctx, torch, prep, steps, warmup, N=2048):
-    """Causal prefill of an N-token prompt through one sliding and one global
-    layer.  The timed steps replay as one captured graph (a graph per step
-    adds a launch gap of about 4 us to each 0.1-0.4 ms step), after
-    `warmup` untimed steps: the clocks need tens of milliseconds of this
-    load to settle (global layer 348 us after 2 warm-up steps, 322 us after
-    50, measured in one process)."""
+def bench_prefill(ctx, torch, prep, steps, warmup, N=2048, want_host=False):
+    """Configuration 4: a causal prefill of an N-token prompt through one
+    sliding and one global layer.  All timed steps replay as one captured
+    graph after at least 50 untimed steps: the clocks need tens of
+    milliseconds of this load to settle (global layer 348 us after 2 warm-up
+    steps, 322 us after 50, measured in one process)."""
+    warmup = max(warmup, 50)
     res = {}
+    host = {}
     total_flops, total_s = 0, 0.0
     for name, d, window, base in (("sliding_d256_W512", 256, WINDOW, LOCAL_BASE), ("global_d512", 512, 0, GLOBAL_BASE)):
         freqs = prep.rope_freqs(d) if not window else None
@@ -189,14 +239,75 @@ def bench_prefill(ctx, torch, prep, steps, warmup, N=2048):
         q = prep.rows(N, d, 0, base, freqs, heads=N_HEADS)
         out = torch.zeros(N * N_HEADS * d, device="cuda")
         wall, ev = time_steps(torch, lambda i: ctx.attend_prefill(q, K, V, 0, N, window, N_HEADS, N_KV, d, out),
-                              steps, warmup, block=steps)
+                              steps, warmup)
         ctx.check_status()
         fl = prefill_flops(N, window, d)
         res[name] = {"us": ev / steps * 1e6, "tflops": fl / (ev / steps) / 1e12, "flops": fl}
         total_flops += fl
         total_s += ev / steps
+        if want_host:
+            host[name] = (q.cpu().numpy(), K.cpu().numpy(), V.cpu().numpy(), window, d)
+        del K, V, q, out
+    res["both_layers_us"] = total_s * 1e6
     res["both_layers_tflops"] = total_flops / total_s / 1e12
     res["frac_of_f32_mfma_peak"] = res["both_layers_tflops"] / F32_MFMA_PEAK_TFLOPS
+    if want_host:
+        res["host"] = host
+    return res
+
+
+def bench_ragged(ctx, torch, prep, steps, warmup, want_host=False):
+    """Configuration 5: the ragged batch, global layer (whole contexts,
+    2.04 GB of K/V, larger than the Infinity Cache: HBM-cold by size) and
+    sliding layer (the last 512 rows of each sequence, 34 MB: resident
+    between steps).  Timed per layer and as the whole step (both layers)."""
+    import numpy as np
+    lens = ragged_lengths()
+    row0 = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int64)
+    total = int(lens.sum())
+    layers = {}
+    host = {}
+    for name, d, glob in (("global_d512", 512, True), ("sliding_d256_W512", 256, False)):
+        freqs = prep.rope_freqs(d) if glob else None
+        base = GLOBAL_BASE if glob else LOCAL_BASE
+        begin = np.array([0 if glob else max(0, int(L) - WINDOW) for L in lens], np.int64)
+        K = prep.rows(total, d, 0, base, freqs)  # positions are not per-sequence here: timing only
+        V = prep.rows(total, d, 0, 0.0, None, rope=False)
+        q = prep.rows(RAGGED_B, d, 0, base, freqs, heads=N_HEADS)
+        out = torch.zeros(RAGGED_B * N_HEADS * d, device="cuda")
+        t_row0, t_b, t_e = (torch.from_numpy(a).cuda() for a in (row0, begin, lens))
+        max_len = int((lens - begin).max())
+        nbytes = sum(decode_bytes(int(lens[s] - begin[s]), d) for s in range(RAGGED_B))
+
+        def call(i, q=q, K=K, V=V, t_row0=t_row0, t_b=t_b, t_e=t_e, max_len=max_len, d=d, out=out):
+            ctx.attend_decode_batch(q, K, V, t_row0, t_b, t_e, max_len, N_HEADS, N_KV, d, out)
+
+        layers[name] = {"call": call, "bytes": nbytes, "keep": (K, V, q, out, t_row0, t_b, t_e)}
+        if want_host:
+            host[name] = (q.cpu().numpy(), K.cpu().numpy(), V.cpu().numpy(), begin.copy(), d)
+    res = {}
+    for name, L in layers.items():
+        wall, ev = time_steps(torch, L["call"], steps, warmup)
+        ctx.check_status()
+        res[name] = {"us": ev / steps * 1e6, "gbs": L["bytes"] / (ev / steps) / 1e9, "bytes": L["bytes"],
+                     "frac_of_hbm_peak": L["bytes"] / (ev / steps) / 1e9 / HBM_PEAK_GBS}
+
+    def step(i):
+        for L in layers.values():
+            L["call"](i)
+
+    wall, ev = time_steps(torch, step, steps, warmup)
+    ctx.check_status()
+    nbytes = sum(L["bytes"] for L in layers.values())
+    res["step"] = {"us": ev / steps * 1e6, "wall_us": wall / steps * 1e6, "bytes": nbytes,
+                   "gbs": nbytes / (ev / steps) / 1e9}
+    res["lengths"] = {"min": int(lens.min()), "max": int(lens.max()), "mean": float(lens.mean()),
+                      "seed": RAGGED_SEED}
+    res["cache"] = "global layer HBM-cold by size (2.04 GB); sliding layer resident (34 MB re-read every step)"
+    if want_host:
+        res["host"] = {"lens": lens, "layers": host}
+    del layers
+    torch.cuda.empty_cache()
     return res
 
 
@@ -225,7 +336,7 @@ def bench_layer_steps(ctx, torch, prep, steps, warmup, T=4096, N=2048):
         ctx.decode_step_fused(q, k, v, wq, wk, EPS, GLOBAL_BASE, freqs, T - 1, K, V, N_KV * d, T, k_row, v_row,
                               N_HEADS, N_KV, d, out)
 
-    wall, ev = time_steps(torch, fused, steps, warmup, block=20)
+    wall, ev = time_steps(torch, fused, steps, warmup)
     ctx.check_status()
     res["decode_global_d512_ctx4096_layer_step"] = {"us_per_layer": ev / steps * 1e6,
                                                     "wall_us_per_layer": wall / steps * 1e6,
@@ -238,7 +349,7 @@ def bench_layer_steps(ctx, torch, prep, steps, warmup, T=4096, N=2048):
                         k_rows=k_row, v_rows=v_row, row_stride=N_KV * d)
         ctx.attend_decode(q, K, V, 0, T, N_HEADS, N_KV, d, out)
 
-    wall, ev = time_steps(torch, two_launch, steps, warmup, block=20)
+    wall, ev = time_steps(torch, two_launch, steps, warmup)
     ctx.check_status()
     res["decode_global_d512_ctx4096_two_launch_step"] = {
         "us_per_layer": ev / steps * 1e6,
@@ -259,7 +370,7 @@ def bench_layer_steps(ctx, torch, prep, steps, warmup, T=4096, N=2048):
                             row_stride=N_KV * d)
             ctx.attend_prefill(q, Kc, Vc, 0, N, window, N_HEADS, N_KV, d, out)
 
-        wall, ev = time_steps(torch, pstep, psteps, max(2, warmup // 4), block=psteps)
+        wall, ev = time_steps(torch, pstep, psteps, max(2, warmup // 4))
         ctx.check_status()
         fl = prefill_flops(N, window, d)
         res[f"prefill_2048_{name}_layer"] = {"us": ev / psteps * 1e6, "tflops": fl / (ev / psteps) / 1e12}
@@ -292,7 +403,7 @@ def bench_matvec(ctx, torch, steps, warmup, rows=262144, cols=1536, cap=30.0):
             else:
                 ctx.logits_q8_0(w, r, c, x, softcap, out)
 
-        wall, ev = time_steps(torch, step, steps, warmup, block=10)
+        wall, ev = time_steps(torch, step, steps, warmup)
         nbytes = r * nb * 34 + c * 4 + r * 4
         res[name] = {"us": ev / steps * 1e6, "gbs": nbytes / (ev / steps) / 1e9, "bytes": nbytes,
                      "frac_of_hbm_peak": nbytes / (ev / steps) / 1e9 / HBM_PEAK_GBS}
@@ -300,31 +411,42 @@ def bench_matvec(ctx, torch, steps, warmup, rows=262144, cols=1536, cap=30.0):
     return res
 
 
-def bench_ragged(ctx, torch, prep, steps, warmup, B=32, seed=2024):
-    import numpy as np
-    lens = np.random.default_rng(seed).integers(1024, 32768 + 1, size=B).astype(np.int64)
+def floors_lib():
+    path = os.path.join(ROOT, "gemma4-rs_amd", "lib", "libg4floors.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'`")
+    lib = ctypes.CDLL(path)
+    lib.g4f_empty.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    lib.g4f_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    return lib
+
+
+def bench_floors(torch, steps, warmup):
+    """The floors the decode kernels are measured against: an empty kernel
+    of 256 workgroups x 512 threads (the decode split grid's shape) per
+    launch in a captured graph, and streaming reads of 1 MiB (a sliding
+    layer's K/V, resident), 16 MiB (a 4096-key global layer's, HBM-cold:
+    copies rotated) and 1 GiB (HBM-cold by size), each one launch of
+    2048 x 256 threads with 16-byte non-temporal loads."""
+    lib = floors_lib()
+
+    def check(rc):
+        if rc:
+            raise RuntimeError("floors kernel launch failed")
+
+    stream = lambda: torch.cuda.current_stream().cuda_stream
     res = {}
-    for name, d, glob in (("global_d512", 512, True), ("sliding_d256_W512", 256, False)):
-        freqs = prep.rope_freqs(d) if glob else None
-        base = GLOBAL_BASE if glob else LOCAL_BASE
-        row0 = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int64)
-        begin = np.array([0 if glob else max(0, int(L) - WINDOW) for L in lens], np.int64)
-        total = int(lens.sum())
-        K = prep.rows(total, d, 0, base, freqs)  # positions are not per-sequence here: timing only
-        V = prep.rows(total, d, 0, 0.0, None, rope=False)
-        q = prep.rows(B, d, 0, base, freqs, heads=N_HEADS)
-        out = torch.zeros(B * N_HEADS * d, device="cuda")
-        t_row0, t_b, t_e = (torch.from_numpy(a).cuda() for a in (row0, begin, lens))
-        max_len = int((lens - begin).max())
-        wall, ev = time_steps(torch, lambda i: ctx.attend_decode_batch(q, K, V, t_row0, t_b, t_e, max_len, N_HEADS,
-                                                                       N_KV, d, out), steps, warmup)
-        ctx.check_status()
-        nbytes = sum(decode_bytes(int(lens[s] - begin[s]), d) for s in range(B))
-        res[name] = {"us": ev / steps * 1e6, "gbs": nbytes / (ev / steps) / 1e9, "bytes": nbytes,
-                     "frac_of_hbm_peak": nbytes / (ev / steps) / 1e9 / HBM_PEAK_GBS}
-        del K, V
-        torch.cuda.empty_cache()
-    res["lengths"] = {"min": int(lens.min()), "max": int(lens.max()), "mean": float(lens.mean())}
+    wall, ev = time_steps(torch, lambda i: check(lib.g4f_empty(256, 512, stream())), steps, warmup)
+    res["empty_kernel_256x512"] = {"us_per_launch": ev / steps * 1e6}
+    sink = torch.zeros(2048, device="cuda")
+    for name, nbytes, copies in (("read_1MiB_resident", 1 << 20, 1), ("read_16MiB_cold", 16 << 20, 24),
+                                 ("read_1GiB", 1 << 30, 1)):
+        bufs = [torch.ones(nbytes // 4, device="cuda") for _ in range(copies)]
+        wall, ev = time_steps(torch, lambda i: check(lib.g4f_read(bufs[i % copies].data_ptr(), nbytes,
+                                                                  sink.data_ptr(), 2048, stream())), steps, warmup)
+        res[name] = {"us": ev / steps * 1e6, "gbs": nbytes / (ev / steps) / 1e9}
+        del bufs
+    torch.cuda.empty_cache()
     return res
 
 
@@ -338,62 +460,220 @@ def bench_copy(torch, steps, nbytes=256 << 20):
             "gbs": 2 * nbytes / (ev / steps) / 1e9}
 
 
-def measured_traffic(profile="decode_global_d512_ctx4096.txt"):
-    """HBM bytes per decode step (split + merge kernels) from the committed
-    rocprofv3 FETCH_SIZE / WRITE_SIZE summary, or None if it is absent."""
-    path = os.path.join(ROOT, "profiles", profile)
+# ------------------------------------------------------------- profiles/
+def profile_summary(name):
+    """Per-kernel figures from a committed profiles/ summary: {kernel:
+    {"avg_us": ..., "read_mb": ..., "written_mb": ..., counters...}}."""
+    path = os.path.join(ROOT, "profiles", name)
+    out = {}
     if not os.path.exists(path):
-        return None
-    total = 0.0
+        return out
+    section = None
     for line in open(path):
-        f = line.split()
-        if len(f) >= 3 and "decode_" in line and "_kernel" in line:
-            try:
-                total += (float(f[-2]) + float(f[-1])) * 1e6
-            except ValueError:
-                continue
-    return int(total) if total else None
+        s = line.strip()
+        if s.startswith("kernel") and "avg us" in s:
+            section = "trace"
+            continue
+        if s.startswith("kernel") and "read MB" in s:
+            section = "bytes"
+            continue
+        if s.startswith("kernel") and "mfma busy" in s:
+            section = "mfma"
+            continue
+        if not s or not (s.startswith("void g4::") or s.startswith("g4::")):
+            if not s:
+                section = None
+            continue
+        f = s.split()
+        try:
+            if section == "trace":
+                out.setdefault(" ".join(f[:-3]), {})["avg_us"] = float(f[-2])
+            elif section == "bytes":
+                d = out.setdefault(" ".join(f[:-2]), {})
+                d["read_mb"], d["written_mb"] = float(f[-2]), float(f[-1])
+            elif section == "mfma":
+                d = out.setdefault(" ".join(f[:-2]), {})
+                d["mfma_busy"], d["mfma_tflops"] = float(f[-2]), float(f[-1])
+        except ValueError:
+            continue
+    return out
 
 
-def cpu_baseline(host, bytes_per_step, seconds):
-    """The oracle's attend over the same K/V, with the reference's per-row
-    `concat` copy and per-head pool, timed for about `seconds`."""
-    import numpy as np
-    from oracle import pyoracle as orc
+def traffic_bytes(name, kernels=None):
+    """HBM bytes (read + written) per step from a profiles/ summary: of the
+    named kernels (substring match, one dispatch each), or with kernels None
+    the summary's whole-step total (every dispatch of a step); None when the
+    summary does not hold them."""
+    if kernels is None:
+        path = os.path.join(ROOT, "profiles", name)
+        if not os.path.exists(path):
+            return None
+        for line in open(path):
+            f = line.split()
+            if line.strip().startswith("per step: read"):
+                return int((float(f[3]) + float(f[6])) * 1e6)
+        return None
+    prof = profile_summary(name)
+    total, found = 0.0, False
+    for k, v in prof.items():
+        if any(sub in k for sub in kernels) and "read_mb" in v:
+            total += (v["read_mb"] + v["written_mb"]) * 1e6
+            found = True
+    return int(total) if found else None
 
-    q = np.ascontiguousarray(host["q"].reshape(-1))
-    rows = orc.RowPointers(np.ascontiguousarray(host["K"]), np.ascontiguousarray(host["V"]))
-    out = np.zeros_like(q)
-    pool = orc.pool_threads()
-    threads_used = min(pool, N_HEADS)  # attention hands out one head per chunk (pool.rs:170-171)
-    res = {}
-    for label, threads in (("pool", 0), ("single_thread", 1)):
-        rows.attend(q, 0, rows.T, N_HEADS, N_KV, out, threads=threads)  # warm
+
+# ---------------------------------------------------------- CPU baseline
+class CpuTimer:
+    """Times the oracle's attend (the reference's attend with its `concat`
+    copy and per-head pool) on this host's cores."""
+
+    def __init__(self):
+        from oracle import pyoracle as orc
+        self.orc = orc
+        self.pool = orc.pool_threads()
+        self.threads = min(self.pool, N_HEADS)  # one head per chunk (pool.rs:170-171)
+
+    def loop(self, fn, seconds, min_calls=2):
+        fn()  # warm
         n, t0 = 0, time.perf_counter()
         while True:
-            rows.attend(q, 0, rows.T, N_HEADS, N_KV, out, threads=threads)
+            fn()
             n += 1
             el = time.perf_counter() - t0
-            if (el >= seconds / 2 and n >= 3) or el >= seconds:
-                break
-        res[label] = {"us_per_step": el / n * 1e6, "gbs": bytes_per_step / (el / n) / 1e9, "calls": n}
-    return res, threads_used
+            if (n >= min_calls and el >= seconds) or el >= 4 * seconds:
+                return el / n, n
+
+    def rows(self, K, V):
+        import numpy as np
+        return self.orc.RowPointers(np.ascontiguousarray(K), np.ascontiguousarray(V))
+
+
+def cpu_decode(cpu, host, T, nbytes, seconds):
+    """Configurations 1 and 2: attend over T rows."""
+    import numpy as np
+    q = np.ascontiguousarray(host["q"].reshape(-1))
+    rows = cpu.rows(host["K"], host["V"])
+    out = np.zeros_like(q)
+    s, n = cpu.loop(lambda: rows.attend(q, 0, T, N_HEADS, N_KV, out), seconds)
+    s1, n1 = cpu.loop(lambda: rows.attend(q, 0, T, N_HEADS, N_KV, out, threads=1), seconds / 2)
+    return {"value": round(nbytes / s / 1e9, 4), "unit": "GB/s", "us_per_layer": round(s * 1e6, 1),
+            "cores": cpu.threads, "kind": "port",
+            "sample": f"{n} calls of the same step; single thread {nbytes / s1 / 1e9:.3f} GB/s "
+                      f"({s1 * 1e6:.0f} us/step); host has {os.cpu_count()} logical CPUs"}
+
+
+def cpu_stack(cpu, host, nbytes, seconds):
+    """Configuration 3: the reference's layer loop, one attend per layer
+    over its source layer's rows (model.rs:407-410)."""
+    import numpy as np
+    rows = {l: cpu.rows(K, V) for l, (K, V) in host["kv"].items()}
+    qs = [np.ascontiguousarray(q.reshape(-1)) for q in host["q"]]
+    outs = [np.zeros_like(q) for q in qs]
+
+    def stack():
+        for (layer, src, b, e, d, glob), q, out in zip(host["plan"], qs, outs):
+            rows[src].attend(q, b, e, N_HEADS, N_KV, out)
+
+    s, n = cpu.loop(stack, seconds)
+    return {"value": round(nbytes / s / 1e9, 4), "unit": "GB/s", "us_per_stack": round(s * 1e6, 1),
+            "cores": cpu.threads, "kind": "port",
+            "sample": f"{n} whole stacks (35 attend calls each, resident in host memory); "
+                      f"host has {os.cpu_count()} logical CPUs"}
+
+
+def cpu_prefill(cpu, host, seconds, stride=8):
+    """Configuration 4: the reference's prompt loop, one attend per token
+    (crates/llm-gemma4/src/impl_/generate.rs:37-41), on every `stride`-th
+    position of the 2048-token prompt; TFLOP/s from the sampled positions'
+    own FLOPs."""
+    import numpy as np
+    res = {}
+    tot_fl, tot_s = 0, 0.0
+    for name, (q, K, V, window, d) in host.items():
+        rows = cpu.rows(K, V)
+        N = q.shape[0]
+        pos = list(range(stride - 1, N, stride))
+        qs = [np.ascontiguousarray(q[i]) for i in pos]
+        out = np.zeros(N_HEADS * d, np.float32)
+        ranges = [(max(0, i + 1 - window) if window else 0, i + 1) for i in pos]
+        fl = sum(4 * N_HEADS * d * (e - b) for b, e in ranges)
+
+        def prompt():
+            for qi, (b, e) in zip(qs, ranges):
+                rows.attend(qi, b, e, N_HEADS, N_KV, out)
+
+        s, n = cpu.loop(prompt, seconds / 2, min_calls=1)
+        res[name] = {"tflops": fl / s / 1e12, "us_per_token": s / len(pos) * 1e6}
+        tot_fl += fl
+        tot_s += s
+    return {"value": round(tot_fl / tot_s / 1e12, 6), "unit": "TFLOP/s", "cores": cpu.threads, "kind": "port",
+            "layers": res,
+            "sample": f"the prompt loop at every {stride}th position (256 of 2048 tokens per layer, their own "
+                      f"FLOPs); host has {os.cpu_count()} logical CPUs"}
+
+
+def cpu_ragged(cpu, host, nbytes, seconds):
+    """Configuration 5: the reference's engine is single-sequence, so the
+    batch is a loop over the 32 sequences, one attend each per layer."""
+    import numpy as np
+    lens = host["lens"]
+    row0 = np.concatenate([[0], np.cumsum(lens)[:-1]])
+    calls = []
+    for name, (q, K, V, begin, d) in host["layers"].items():
+        rows = cpu.rows(K, V)
+        outs = np.zeros(N_HEADS * d, np.float32)
+        for s in range(len(lens)):
+            calls.append((rows, np.ascontiguousarray(q[s]), int(row0[s] + begin[s]), int(row0[s] + lens[s]), outs))
+
+    def batch():
+        for rows, q, b, e, out in calls:
+            rows.attend(q, b, e, N_HEADS, N_KV, out)
+
+    s, n = cpu.loop(batch, seconds, min_calls=1)
+    return {"value": round(nbytes / s / 1e9, 4), "unit": "GB/s", "us_per_step": round(s * 1e6, 1),
+            "cores": cpu.threads, "kind": "port",
+            "sample": f"{n} whole steps (64 attend calls: 32 sequences x 2 layers); host has "
+                      f"{os.cpu_count()} logical CPUs"}
+
+
+# ------------------------------------------------------------------ main
+ONLY = ["sliding", "global", "stack", "stackwarm", "prefill", "ragged", "layer", "matvec", "floors", "copy"]
+
+
+def run_only(args, torch, g4hip):
+    with g4hip.Context(0) as ctx:
+        prep = Prep(ctx, torch, 1234)
+        k = max(20, args.steps // 4)
+        fn = {"sliding": lambda: bench_sliding_decode(ctx, torch, prep, args.steps, args.warmup),
+              "global": lambda: bench_global_decode(ctx, torch, prep, args.steps, args.warmup),
+              "stack": lambda: bench_stack(ctx, torch, prep, g4hip, k, 5, cold=True),
+              "stackwarm": lambda: bench_stack(ctx, torch, prep, g4hip, k, 5, cold=False),
+              "prefill": lambda: bench_prefill(ctx, torch, prep, min(args.steps, 20), args.warmup),
+              "ragged": lambda: bench_ragged(ctx, torch, prep, max(5, k // 4), 2),
+              "layer": lambda: bench_layer_steps(ctx, torch, prep, args.steps, args.warmup),
+              "matvec": lambda: bench_matvec(ctx, torch, max(20, k // 2), args.warmup),
+              "floors": lambda: bench_floors(torch, max(20, k), 5),
+              "copy": lambda: bench_copy(torch, max(5, k // 4))}[args.only]
+        res = fn()
+        res.pop("host", None)
+        print(json.dumps({"only": args.only, "result": res}))
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=400)
-    ap.add_argument("--warmup", type=int, default=40)
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--no-workloads", action="store_true", help="only the headline step")
-    ap.add_argument("--only", choices=["global", "sliding", "stack", "prefill", "ragged", "layer", "matvec", "copy"],
-                    help="run one workload alone (for profiling); prints its result.  'copy' is a "
-                         "plain 256 MiB device copy, the reference point for HBM byte counters")
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--cpu-seconds", type=float, default=3.0,
+                    help="CPU-baseline sample per configuration (seconds, about)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--only", choices=ONLY,
+                    help="run one workload alone (for profiling) and print its result; 'copy' is a plain "
+                         "256 MiB device copy, the reference point for HBM byte counters")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: the backend runs on a single MI355X (asked for --gpus {args.gpus}).",
-              file=sys.stderr)
+        print(f"bench.py measures one GPU: the backend runs on a single MI355X, and no run here uses a second "
+              f"(asked for --gpus {args.gpus}).", file=sys.stderr)
         sys.exit(2)
 
     import torch
@@ -401,70 +681,111 @@ def main():
 
     torch.cuda.init()
     if args.only:
-        with g4hip.Context(0) as ctx:
-            prep = Prep(ctx, torch, 1234)
-            k = max(20, args.steps // 4)
-            fn = {"global": lambda: bench_global_decode(ctx, torch, prep, args.steps, args.warmup),
-                  "sliding": lambda: bench_sliding_decode(ctx, torch, prep, args.steps, args.warmup),
-                  "stack": lambda: bench_stack(ctx, torch, prep, g4hip, k, 5),
-                  "prefill": lambda: bench_prefill(ctx, torch, prep, max(5, k // 10), args.warmup),
-                  "ragged": lambda: bench_ragged(ctx, torch, prep, max(5, k // 4), 2),
-                  "layer": lambda: bench_layer_steps(ctx, torch, prep, args.steps, args.warmup),
-                  "matvec": lambda: bench_matvec(ctx, torch, max(20, k // 2), args.warmup),
-                  "copy": lambda: bench_copy(torch, max(5, k // 4))}[args.only]
-            res = fn()
-            res.pop("host", None)
-            print(json.dumps({"only": args.only, "result": res}))
+        run_only(args, torch, g4hip)
         return
+    steps, warmup = args.steps, args.warmup
+    k = max(20, steps // 4)
+    want = not args.no_cpu
     with g4hip.Context(0) as ctx:
         prep = Prep(ctx, torch, 1234)
-        g = bench_global_decode(ctx, torch, prep, args.steps, args.warmup)
-        step_s = g["event"] / args.steps
-        achieved = g["bytes"] / step_s / 1e9
-        workloads = {}
-        if not args.no_workloads:
-            k = max(20, args.steps // 4)
-            workloads["sliding_decode_d256_ctx64"] = bench_sliding_decode(ctx, torch, prep, args.steps, args.warmup)
-            workloads["e2b_stack_35_layers_ctx8192"] = bench_stack(ctx, torch, prep, g4hip, k, 5)
-            workloads["prefill_2048"] = bench_prefill(ctx, torch, prep, max(5, k // 10), args.warmup)
-            workloads["ragged_decode_B32"] = bench_ragged(ctx, torch, prep, max(5, k // 4), 2)
-            workloads["layer_drivers"] = bench_layer_steps(ctx, torch, prep, args.steps, args.warmup)
-            workloads["q8_0_matvec"] = bench_matvec(ctx, torch, max(20, k // 2), args.warmup)
-        workloads["global_decode_d512_ctx4096_warm"] = {
-            "us_per_layer": g["event_warm"] / args.steps * 1e6,
-            "gbs": g["bytes"] / (g["event_warm"] / args.steps) / 1e9,
-            "note": "one resident K/V copy, served from the Infinity Cache"}
-        cpu, threads_used = cpu_baseline(g["host"], g["bytes"], args.cpu_seconds)
+        c5 = bench_ragged(ctx, torch, prep, steps, warmup, want_host=want)
+        c1 = bench_sliding_decode(ctx, torch, prep, steps, warmup)
+        c2 = bench_global_decode(ctx, torch, prep, steps, warmup)
+        c3 = bench_stack(ctx, torch, prep, g4hip, k, 5, cold=True)
+        c3w = bench_stack(ctx, torch, prep, g4hip, k, 5, cold=False, want_host=want)
+        c4 = bench_prefill(ctx, torch, prep, min(steps, 20), warmup, want_host=want)
+        workloads = {"layer_drivers": bench_layer_steps(ctx, torch, prep, steps, warmup),
+                     "q8_0_matvec": bench_matvec(ctx, torch, max(20, k // 2), warmup),
+                     "floors": bench_floors(torch, k, 5)}
+    cpu = {}
+    if want:
+        timer = CpuTimer()
+        sec = args.cpu_seconds
+        cpu["5"] = cpu_ragged(timer, c5["host"], c5["step"]["bytes"], sec)
+        cpu["1"] = cpu_decode(timer, c1["host"], 64, c1["bytes"], sec / 2)
+        cpu["2"] = cpu_decode(timer, c2["host"], 4096, c2["bytes"], sec)
+        cpu["3"] = cpu_stack(timer, c3w["host"], c3w["bytes_per_stack"], sec)
+        cpu["4"] = cpu_prefill(timer, c4["host"], sec)
+    for r in (c1, c2, c3w, c4, c5):
+        r.pop("host", None)
 
+    # The headline: configuration 5, both layers per step.
+    step_s = c5["step"]["us"] * 1e-6
+    g5 = c5["global_d512"]
+    prof5 = "decode_ragged_b32_ctx1k-32k.txt"
+    headline_roof = roofline_hbm(g5["bytes"], g5["us"] * 1e-6,
+                                 traffic_bytes(prof5, ["decode_stream_kernel<512", "decode_merge_kernel<3, 512"]),
+                                 kernel="global layer of the batch: decode_stream_kernel<512> + its merge",
+                                 bytes_per_launch=g5["bytes"], us_per_launch=round(g5["us"], 3),
+                                 traffic_source=f"profiles/{prof5} (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, scaled "
+                                                "by profiles/hbm_counter_calibration.txt)")
+    prof2 = "decode_global_d512_ctx4096.txt"
+    prof3 = "decode_e2b_stack_35_layers_ctx8192.txt"
+    prof4 = profile_summary("prefill_2048_sliding_and_global.txt")
+    mfma = {k2: v for k2, v in prof4.items() if "prefill_kernel" in k2 and "mfma_busy" in v}
+    configs = {
+        "1_sliding_decode_d256_ctx64": {
+            "us_per_layer": round(c1["us_per_layer"], 3), "wall_us_per_layer": round(c1["wall_us_per_layer"], 3),
+            "cache": c1["cache"],
+            "roofline": roofline_hbm(c1["bytes"], c1["us_per_layer"] * 1e-6,
+                                     traffic_bytes("decode_sliding_d256_ctx64.txt"),
+                                     bytes_per_launch=c1["bytes"], note="launch-latency-bound: 147 KB per call"),
+            "cpu_baseline": cpu.get("1")},
+        "2_global_decode_d512_ctx4096": {
+            "us_per_layer": round(c2["us_per_layer"], 3), "wall_us_per_layer": round(c2["wall_us_per_layer"], 3),
+            "us_per_layer_resident": round(c2["us_per_layer_resident"], 3), "cache": c2["cache"],
+            "roofline": roofline_hbm(c2["bytes"], c2["us_per_layer"] * 1e-6, traffic_bytes(prof2),
+                                     bytes_per_launch=c2["bytes"], kernel="decode_split_kernel<512> + merge"),
+            "cpu_baseline": cpu.get("2")},
+        "3_e2b_stack_35_layers_ctx8192": {
+            "us_per_stack": round(c3["us_per_stack"], 2), "us_per_layer_mean": round(c3["us_per_layer_mean"], 3),
+            "wall_us_per_stack": round(c3["wall_us_per_stack"], 2), "cache": c3["cache"],
+            "us_per_stack_resident": round(c3w["us_per_stack"], 2),
+            "bytes_per_stack": c3["bytes_per_stack"], "unique_bytes_per_stack": c3["unique_bytes_per_stack"],
+            "roofline": roofline_hbm(c3["bytes_per_stack"], c3["us_per_stack"] * 1e-6,
+                                     traffic_bytes(prof3), bytes_per_launch=c3["bytes_per_stack"],
+                                     note="35 calls (70 launches); bytes count every layer's rows once, "
+                                          "shared layers re-reading layers 13/14"),
+            "cpu_baseline": cpu.get("3")},
+        "4_prefill_2048": {
+            "sliding_d256_W512": {k2: round(v, 3) for k2, v in c4["sliding_d256_W512"].items()},
+            "global_d512": {k2: round(v, 3) for k2, v in c4["global_d512"].items()},
+            "both_layers_us": round(c4["both_layers_us"], 2),
+            "roofline": {"bound": "mfma", "achieved": round(c4["both_layers_tflops"], 2),
+                         "peak": F32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(c4["frac_of_f32_mfma_peak"], 4),
+                         "traffic": None, "dtype": "f32 MFMA (v_mfma_f32_16x16x4f32)",
+                         "mfma_busy_counter": {k2: v["mfma_busy"] for k2, v in mfma.items()} or None,
+                         "mfma_source": "profiles/prefill_2048_sliding_and_global.txt (SQ_VALU_MFMA_BUSY_CYCLES)"},
+            "cpu_baseline": cpu.get("4")},
+        "5_ragged_decode_b32": {
+            "global_d512": {k2: round(v, 4) for k2, v in c5["global_d512"].items()},
+            "sliding_d256_W512": {k2: round(v, 4) for k2, v in c5["sliding_d256_W512"].items()},
+            "step_us": round(c5["step"]["us"], 2), "lengths": c5["lengths"], "cache": c5["cache"],
+            "roofline": headline_roof, "cpu_baseline": cpu.get("5")},
+    }
     line = {
-        "metric": "decode-attn µs/layer + achieved HBM GB/s; prefill-attn TFLOP/s (1× MI355X)",
-        "value": round(achieved, 2),
+        "metric": METRIC,
+        "value": round(c5["step"]["gbs"], 2),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(g["wall"] / args.steps * 1e3, 6),
-        "us_per_layer": round(step_s * 1e6, 3),
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(c5["step"]["wall_us"] * 1e-3, 6),
+        "us_per_layer": {"global_d512": round(g5["us"], 3), "sliding_d256_W512": round(c5["sliding_d256_W512"]["us"], 3)},
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": "global-layer decode attention, 8 q heads / 1 kv head, head_dim 512, context 4096, "
-                               "proportional NEOX RoPE inputs", "context": 4096, "head_dim": 512, "n_heads": N_HEADS,
-                   "n_kv_heads": N_KV, "kv_copies_rotated": g["copies"], "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                     "kernel": "decode step: split-K kernel + merge kernel",
-                     "bytes_per_launch": g["bytes"],
-                     "traffic_source": "profiles/decode_global_d512_ctx4096.txt (rocprofv3 --pmc, "
-                                       "scaled by profiles/hbm_counter_calibration.txt)"},
-        "cpu_baseline": {"value": round(cpu["pool"]["gbs"], 3), "unit": "GB/s", "cores": threads_used,
-                         "kind": "port",
-                         "sample": f"{cpu['pool']['calls']} calls of the same step (us/step "
-                                   f"{cpu['pool']['us_per_step']:.0f}); single thread "
-                                   f"{cpu['single_thread']['gbs']:.3f} GB/s ({cpu['single_thread']['us_per_step']:.0f}"
-                                   f" us/step); host has {os.cpu_count()} logical CPUs"},
+        "config": {"workload": "ragged decode: 32 sequences with context lengths U[1024, 32768] (seed 2024), one "
+                               "token each, through a global layer (head_dim 512, whole contexts) and a sliding "
+                               "layer (head_dim 256, window 512), 8 q heads / 1 kv head, one launch per layer",
+                   "batch": RAGGED_B, "head_dims": [512, 256], "n_heads": N_HEADS, "n_kv_heads": N_KV,
+                   "parallelism": "single GPU"},
+        "roofline": headline_roof,
+        "cpu_baseline": cpu.get("5"),
+        "configs": configs,
         "workloads": workloads,
     }
     print(json.dumps(line))
