@@ -266,6 +266,37 @@ def test_attend_failures_match_the_reference():
     assert np.all(np.isfinite(out))
 
 
+@pytest.mark.parametrize("n_heads,n_kv,d,pos0,N,window", [(4, 2, 8, 0, 24, 0), (4, 2, 8, 7, 20, 5),
+                                                        (8, 1, 16, 3, 30, 8), (8, 1, 16, 0, 12, 1)])
+def test_attend_prefill_is_the_token_loop(n_heads, n_kv, d, pos0, N, window):
+    """or_attend_prefill (the prompt run one token at a time, generate.rs:37-41)
+    equals attend over each query's range, bit for bit, on any thread count;
+    the range [p+1-W or 0, p+1) is the decode's (eng/mod.rs:10-36), and a
+    NaN key fails exactly the queries that attend its row."""
+    rng = np.random.default_rng(pos0 * 31 + N + window)
+    q = rng.standard_normal((N, n_heads * d)).astype(np.float32)
+    K = rng.standard_normal((pos0 + N, n_kv * d)).astype(np.float32)
+    V = rng.standard_normal((pos0 + N, n_kv * d)).astype(np.float32)
+    out, status = orc.attend_prefill(q, K, V, pos0, window, n_heads, n_kv, threads=1)
+    assert not status.any()
+    for i in range(N):
+        p = pos0 + i
+        b = max(0, p + 1 - window) if window else 0
+        assert np.array_equal(out[i], orc.attend(q[i], K[b:p + 1], V[b:p + 1], n_heads, n_kv)), i
+        assert np.max(np.abs(out[i] - f64_attention(q[i], K[b:p + 1], V[b:p + 1], n_heads, n_kv, 1.0))) < 1e-5
+    out3, status3 = orc.attend_prefill(q, K, V, pos0, window, n_heads, n_kv, threads=3)
+    assert np.array_equal(out3, out) and not status3.any()
+    # NaN in key row r: queries at positions p >= r whose window still holds r fail.
+    r = pos0 + N // 2
+    Kb = K.copy()
+    Kb[r, 0] = np.nan
+    _, st = orc.attend_prefill(q, Kb, V, pos0, window, n_heads, n_kv, threads=2)
+    for i in range(N):
+        p = pos0 + i
+        sees = r <= p and (window == 0 or r > p - window)
+        assert bool(st[i]) == sees, (i, st[i])
+
+
 def test_layer_attention_segment_matches_its_parts():
     """or_layer_attention (model.rs:386-411) equals norm -> rope -> append ->
     view -> window -> attend done by hand, and reports the attended set."""
