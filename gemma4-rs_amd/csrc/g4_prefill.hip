@@ -282,39 +282,61 @@ __device__ __forceinline__ void prefill_unit(const PrefillK &p, const PrefillUni
         const bool live = S::KSPLIT == 1 || tw < u.t_hi;  // one group: a step's tile is always live
         const f32x4 *kt = kb + kpar * TILE_F4;
         constexpr int NL = 2 * PER_THREAD * TPS;  // tile-part loads per step
-        // Partial S^T over this wave's DH dims: two independent chains.
+        // Load i: tile i / (2 PER_THREAD) of the next step, part i % (2 PER_THREAD).
+        auto load = [&](int i) {
+            const int j = i / (2 * PER_THREAD);
+            issue_part(tn[j], i % (2 * PER_THREAD), kn + j * TILE_F4, vn + j * TILE_F4);
+        };
+        // Partial S^T over this wave's DH dims: two independent chains.  A
+        // chunk's K operands are read from LDS one chunk ahead, into the other
+        // of two register slots, so the MFMAs of chunk uu run while chunk
+        // uu+1's reads are in flight (one slot made every chunk wait for its
+        // own LDS read).  A group whose tile is stale (the unit's last step
+        // with an odd tile count) only issues its share of the next loads:
+        // its scores are all masked below.
         f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int uu = 0; uu < NU; ++uu) {
-            // The next tile's loads go out one or two per 8 MFMAs, so that
-            // they issue while the matrix pipe works rather than queue up
-            // behind each other at the top of the step.
-            static_assert(NL % NU == 0 || NU % NL == 0, "loads spread over the chunks");
-            // Load i: tile i / (2 PER_THREAD) of the next step, part i % (2 PER_THREAD).
-            auto load = [&](int i) {
-                const int j = i / (2 * PER_THREAD);
-                issue_part(tn[j], i % (2 * PER_THREAD), kn + j * TILE_F4, vn + j * TILE_F4);
+        if (live) {
+            f32x4 kc[2][2];
+            auto read_k = [&](int uu, f32x4(&dst)[2]) {
+                const int ug = d0 / 32 + uu;
+                dst[0] = kt[((ug * 4 + g) * 2 + 0) * 16 + c];
+                dst[1] = kt[((ug * 4 + g) * 2 + 1) * 16 + c];
             };
-            if constexpr (NL >= NU) {
+            read_k(0, kc[0]);
 #pragma unroll
-                for (int i = uu * (NL / NU); i < (uu + 1) * (NL / NU); ++i) load(i);
-            } else if (uu % (NU / NL) == 0) {
-                load(uu / (NU / NL));
+            for (int uu = 0; uu < NU; ++uu) {
+                if (uu + 1 < NU) read_k(uu + 1, kc[(uu + 1) & 1]);
+                // The next tile's loads go out one or two per 8 MFMAs, so that
+                // they issue while the matrix pipe works rather than queue up
+                // behind each other at the top of the step.
+                static_assert(NL % NU == 0 || NU % NL == 0, "loads spread over the chunks");
+                if constexpr (NL >= NU) {
+#pragma unroll
+                    for (int i = uu * (NL / NU); i < (uu + 1) * (NL / NU); ++i) load(i);
+                } else if (uu % (NU / NL) == 0) {
+                    load(uu / (NU / NL));
+                }
+                const f32x4 k0 = kc[uu & 1][0], k1 = kc[uu & 1][1];
+                f32x4 &acc = (uu & 1) ? acc1 : acc0;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k0[j], qreg[uu][j], acc, 0, 0, 0);
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k1[j], qreg[uu][4 + j], acc, 0, 0, 0);
             }
-            const int ug = d0 / 32 + uu;
-            const f32x4 k0 = kt[((ug * 4 + g) * 2 + 0) * 16 + c];
-            const f32x4 k1 = kt[((ug * 4 + g) * 2 + 1) * 16 + c];
-            f32x4 &acc = (uu & 1) ? acc1 : acc0;
+            // Scheduling: chunk 0's K reads, then per chunk the next chunk's K
+            // reads, the next tile's loads (one or two per 8 MFMAs) and the
+            // chunk's 8 MFMAs.
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k0[j], qreg[uu][j], acc, 0, 0, 0);
+            for (int uu = 0; uu < NU; ++uu) {
+                if (uu + 1 < NU) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);       // DS read
+                __builtin_amdgcn_sched_group_barrier(0x010, NL >= NU ? NL / NU : 1, 0);  // VMEM
+                __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);                        // MFMA
+            }
+        } else {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k1[j], qreg[uu][4 + j], acc, 0, 0, 0);
-        }
-        // Scheduling: one load per 8 MFMAs of the chunk loop above.
-#pragma unroll
-        for (int uu = 0; uu < NU; ++uu) {
-            __builtin_amdgcn_sched_group_barrier(0x010, NL >= NU ? NL / NU : 1, 0);  // VMEM
-            __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);                                                // MFMA
+            for (int i = 0; i < NL; ++i) load(i);
         }
         f32x4 sc = acc0 + acc1;
         if constexpr (S::SPLIT == 2) {
@@ -398,16 +420,31 @@ __device__ __forceinline__ void prefill_unit(const PrefillK &p, const PrefillUni
             fix = !(live && whole) && nf_tile[kpar] == tw + 1;
         }
 
-        // O^T += V^T . P^T over the tile's 16 keys (k-step r: keys 4g + r).
+        // O^T += V^T . P^T over the tile's 16 keys (k-step r: keys 4g + r),
+        // operand (r, U) read from LDS one step ahead as the K operands are.
+        if (live) {
+            constexpr int NPV = 4 * NV;
+            f32x4 vc[2];
+            auto read_v = [&](int idx, f32x4 &dst) {
+                const int r = idx / NV, U = idx % NV;
+                dst = vb[kpar * TILE_F4 + (4 * g + r) * (D / 4) + d0 / 4 + 16 * U + c];
+            };
+            read_v(0, vc[0]);
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-#pragma unroll
-            for (int U = 0; U < NV; ++U) {
-                const f32x4 vv = vb[kpar * TILE_F4 + (4 * g + r) * (D / 4) + d0 / 4 + 16 * U + c];
+            for (int idx = 0; idx < NPV; ++idx) {
+                if (idx + 1 < NPV) read_v(idx + 1, vc[(idx + 1) & 1]);
+                const int r = idx / NV, U = idx % NV;
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    o[4 * U + i] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[i], pr[r], o[4 * U + i], 0, 0, 0);
+                    o[4 * U + i] = __builtin_amdgcn_mfma_f32_16x16x4f32(vc[idx & 1][i], pr[r], o[4 * U + i], 0, 0, 0);
             }
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+#pragma unroll
+            for (int idx = 0; idx < NPV; ++idx) {
+                if (idx + 1 < NPV) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+                __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);                      // MFMA
+            }
+        }
 
         if (fix) {
             // Key k = 4kq + r of the tile: its weight for this lane's row c is
