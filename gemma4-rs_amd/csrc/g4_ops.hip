@@ -27,8 +27,7 @@ __global__ __launch_bounds__(256) void rms_norm_rows_kernel(const float *x, int6
         const float sq = v * v;
         sum += (double)sq;
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+    sum = wave_sum_f64(sum);
     const float mean = (float)(sum / (double)width);
     // 1 / sqrt(mean + eps) with the f32 rounding of each step: sqrt and the
     // division are done in f64 and rounded once to f32, which for these two
@@ -136,8 +135,7 @@ __global__ __launch_bounds__(64 * kPrepWaves) void prepare_qkv_kernel(PrepareArg
                 const float sq = xv * xv;
                 sum += (double)sq;
             }
-#pragma unroll
-            for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+            sum = wave_sum_f64(sum);
             const float mean = (float)(sum / (double)d);
             const float root = (float)sqrt((double)(mean + a.eps));
             scale = (float)(1.0 / (double)root);

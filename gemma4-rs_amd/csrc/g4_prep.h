@@ -10,7 +10,44 @@
 
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 namespace g4 {
+
+// Sum over the 64 lanes of a wavefront, in f64, the same bits in every lane:
+// a butterfly whose partners are lane ^ 1, ^ 2 (DPP quad_perm), ^ 7 (DPP
+// row_half_mirror), ^ 8 (DPP row_ror:8), ^ 16 and ^ 32 (permlane swaps); the
+// six masks span the six lane bits.  Both partners of an exchange add the
+// same two values (f64 addition is commutative), so every lane ends with
+// the same sum.  Sums of f32 squares of one row are exact in f64 unless the
+// squares span more than about 2^20, so the order does not change them.
+__device__ __forceinline__ double wave_sum_f64(double v) {
+    auto dpp = [](double x, auto ctrl) {
+        const unsigned long long b = __double_as_longlong(x);
+        const int lo = __builtin_amdgcn_update_dpp(0, (int)(unsigned)b, decltype(ctrl)::value, 0xF, 0xF, false);
+        const int hi = __builtin_amdgcn_update_dpp(0, (int)(unsigned)(b >> 32), decltype(ctrl)::value, 0xF, 0xF, false);
+        return __longlong_as_double((long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo));
+    };
+    v += dpp(v, std::integral_constant<int, 0xB1>{});   // lane ^ 1
+    v += dpp(v, std::integral_constant<int, 0x4E>{});   // lane ^ 2
+    v += dpp(v, std::integral_constant<int, 0x141>{});  // lane ^ 7 within 8
+    v += dpp(v, std::integral_constant<int, 0x128>{});  // lane ^ 8 within 16
+    {
+        const unsigned long long b = __double_as_longlong(v);
+        const auto lo = __builtin_amdgcn_permlane16_swap((unsigned)b, (unsigned)b, false, false);
+        const auto hi = __builtin_amdgcn_permlane16_swap((unsigned)(b >> 32), (unsigned)(b >> 32), false, false);
+        v = __longlong_as_double((long long)(((unsigned long long)hi[0] << 32) | lo[0])) +
+            __longlong_as_double((long long)(((unsigned long long)hi[1] << 32) | lo[1]));
+    }
+    {
+        const unsigned long long b = __double_as_longlong(v);
+        const auto lo = __builtin_amdgcn_permlane32_swap((unsigned)b, (unsigned)b, false, false);
+        const auto hi = __builtin_amdgcn_permlane32_swap((unsigned)(b >> 32), (unsigned)(b >> 32), false, false);
+        v = __longlong_as_double((long long)(((unsigned long long)hi[0] << 32) | lo[0])) +
+            __longlong_as_double((long long)(((unsigned long long)hi[1] << 32) | lo[1]));
+    }
+    return v;
+}
 
 template <int D>
 struct PrepRow {
@@ -67,8 +104,7 @@ __device__ __forceinline__ void prep_compute(PrepRow<D> &r, bool has_w, bool rop
         const float sq = r.x[m] * r.x[m];
         sum += (double)sq;
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+    sum = wave_sum_f64(sum);
     const float mean = (float)(sum / (double)D);
     const float root = (float)sqrt((double)(mean + eps));
     const float scale = (float)(1.0 / (double)root);
