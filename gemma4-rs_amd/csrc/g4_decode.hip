@@ -630,13 +630,14 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::NW) void decode_layer_kernel(D
     __shared__ float sk[NW];
     const bool is_k = ln.wave == 0, prep_kv = fresh && ln.wave < 2;
     PrepRow<D> row, kv;
-    prep_load<D>(row, ln.lane, lp.q + ((int64_t)kvh * NW + ln.wave) * D, lp.q_w, lp.factors, true);
-    prep_load_angles<D>(row, ln.lane, lp.angles);
-    if (prep_kv) {
-        prep_load<D>(kv, ln.lane, (is_k ? lp.k : lp.v) + (int64_t)kvh * D, is_k ? lp.k_w : nullptr, lp.factors,
-                     is_k);
-        if (is_k) prep_load_angles<D>(kv, ln.lane, lp.angles);
-    }
+    prep_load<D>(row, ln.lane, lp.q + ((int64_t)kvh * NW + ln.wave) * D, lp.q_w);
+    if (prep_kv) prep_load<D>(kv, ln.lane, (is_k ? lp.k : lp.v) + (int64_t)kvh * D, is_k ? lp.k_w : nullptr);
+    // Thread i < D/2 builds entry i of the workgroup's RoPE table (shared by
+    // the q heads and k); its angle and divisor load with the rows.
+    static_assert(D / 2 <= 64 * NW, "one table entry per thread");
+    const bool tab = (int)threadIdx.x < D / 2;
+    const float th = tab ? lp.angles[threadIdx.x] : 0.0f;
+    const float fac = (tab && lp.factors) ? lp.factors[threadIdx.x] : 1.0f;
     __builtin_amdgcn_sched_barrier(0);
     PairPipe<D, NBUF, AUX> pp;
     if (n_keys > 0) {
@@ -647,10 +648,15 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::NW) void decode_layer_kernel(D
     }
     __builtin_amdgcn_sched_barrier(0);
     {
-        prep_compute<D>(row, lp.q_w != nullptr, true, lp.eps);
+        __shared__ float rcs[D / 2], rsn[D / 2];
+        if (tab) prep_rope_table(rcs, rsn, threadIdx.x, th, fac);
+        prep_norm<D>(row, lp.q_w != nullptr, lp.eps);
+        if (prep_kv) prep_norm<D>(kv, is_k && lp.k_w != nullptr, lp.eps);
+        __syncthreads();  // the table
+        prep_rope_tab<D>(row, ln.lane, rcs, rsn);
         prep_store<D>(row, ln.lane, qp[ln.wave]);
         if (prep_kv) {
-            prep_compute<D>(kv, is_k && lp.k_w != nullptr, is_k, lp.eps);
+            if (is_k) prep_rope_tab<D>(kv, ln.lane, rcs, rsn);
             prep_store<D>(kv, ln.lane, kvn[ln.wave]);
             prep_store<D>(kv, ln.lane, (is_k ? lp.k_row : lp.v_row) + (int64_t)kvh * D);  // the append
         }

@@ -210,13 +210,30 @@ __global__ __launch_bounds__(64 * kPrepMaxRowsPerGroup) void prepare_heads_kerne
         rope = false;
         if (a.v_rows) cache = a.v_rows + t * a.row_stride + (int64_t)h * D;
     }
+    // The RoPE table (sine and cosine of each pair's angle) is built once per
+    // workgroup and shared by its q and k heads; the divisors are loaded with
+    // the rows.
+    __shared__ float rcs[HALF], rsn[HALF];
+    constexpr int TPT = HALF / 64 > 0 ? HALF / 64 : 1;  // table entries per thread, at most
+    float fac[TPT];
+#pragma unroll
+    for (int k = 0; k < TPT; ++k) {
+        const int i = threadIdx.x + k * blockDim.x;
+        fac[k] = (i < HALF && a.factors) ? a.factors[i] : 1.0f;
+    }
     PrepRow<D> row;
-    if (active) prep_load<D>(row, lane, x, w, a.factors, rope);
+    if (active) prep_load<D>(row, lane, x, w);
     if (threadIdx.x == 0) prep_angles(theta, HALF, a.pos0 + t, a.theta_scale);
     __syncthreads();
+#pragma unroll
+    for (int k = 0; k < TPT; ++k) {
+        const int i = threadIdx.x + k * blockDim.x;
+        if (i < HALF) prep_rope_table(rcs, rsn, i, theta[i], fac[k]);
+    }
+    if (active) prep_norm<D>(row, w != nullptr, a.eps);
+    __syncthreads();
     if (!active) return;
-    if (rope) prep_load_angles<D>(row, lane, theta);
-    prep_compute<D>(row, w != nullptr, rope, a.eps);
+    if (rope) prep_rope_tab<D>(row, lane, rcs, rsn);
     prep_store<D>(row, lane, x);
     if (cache) prep_store<D>(row, lane, cache);
 }

@@ -54,7 +54,7 @@ struct PrepRow {
     static constexpr int E = D / 64;   // elements per lane
     static constexpr int PE = E / 2;   // NEOX pairs per lane
     static constexpr int HALF = D / 2;
-    float x[E], w[E], f[PE], a[PE];  // row, weight, RoPE divisors, angles theta_i
+    float x[E], w[E];  // row, weight
 };
 
 // The angles theta_i = pos * theta_scale^i of rope_neox, by the reference's
@@ -68,36 +68,23 @@ __device__ inline void prep_angles(float *theta, int half, int64_t pos, float th
     }
 }
 
-// Loads row x, its weight w (or none) and the RoPE divisors (or 1).
+// Loads row x and its weight w (or none).
 template <int D>
-__device__ __forceinline__ void prep_load(PrepRow<D> &r, int lane, const float *x, const float *w,
-                                          const float *factors, bool rope) {
+__device__ __forceinline__ void prep_load(PrepRow<D> &r, int lane, const float *x, const float *w) {
 #pragma unroll
     for (int m = 0; m < PrepRow<D>::E; ++m) r.x[m] = x[lane + 64 * m];
     if (w) {
 #pragma unroll
         for (int m = 0; m < PrepRow<D>::E; ++m) r.w[m] = w[lane + 64 * m];
     }
-    if (rope) {
-#pragma unroll
-        for (int m = 0; m < PrepRow<D>::PE; ++m) r.f[m] = factors ? factors[lane + 64 * m] : 1.0f;
-    }
 }
 
-// This lane's angles theta_{lane + 64m} from a table of D/2 (built by
-// prep_angles, or by the same recurrence on the host).
+// rms_norm (f64 mean of squares, ops.rs:45-56) times the weight, in the
+// row's registers.
 template <int D>
-__device__ __forceinline__ void prep_load_angles(PrepRow<D> &r, int lane, const float *theta) {
-#pragma unroll
-    for (int m = 0; m < PrepRow<D>::PE; ++m) r.a[m] = theta[lane + 64 * m];
-}
-
-// rms_norm (f64 mean of squares, ops.rs:45-56) times the weight, then RoPE
-// with the loaded angles, in the row's registers.
-template <int D>
-__device__ __forceinline__ void prep_compute(PrepRow<D> &r, bool has_w, bool rope, float eps) {
+__device__ __forceinline__ void prep_norm(PrepRow<D> &r, bool has_w, float eps) {
 #pragma clang fp contract(off)
-    constexpr int E = PrepRow<D>::E, PE = PrepRow<D>::PE;
+    constexpr int E = PrepRow<D>::E;
     double sum = 0.0;
 #pragma unroll
     for (int m = 0; m < E; ++m) {
@@ -113,16 +100,27 @@ __device__ __forceinline__ void prep_compute(PrepRow<D> &r, bool has_w, bool rop
         r.x[m] = r.x[m] * scale;
         if (has_w) r.x[m] = r.x[m] * r.w[m];
     }
-    if (rope) {
+}
+
+// Entry i of a token's RoPE table: the sine and cosine of pair i's angle
+// theta_i / f_i (rope_neox, ops.rs:134-162), computed once per workgroup
+// and shared by all of the token's heads.
+__device__ __forceinline__ void prep_rope_table(float *cs, float *sn, int i, float theta, float factor) {
+#pragma clang fp contract(off)
+    sincosf(theta / factor, &sn[i], &cs[i]);
+}
+
+// The NEOX rotation of the row's pairs (i, i + D/2) by the table's angles.
+template <int D>
+__device__ __forceinline__ void prep_rope_tab(PrepRow<D> &r, int lane, const float *cs, const float *sn) {
+#pragma clang fp contract(off)
+    constexpr int PE = PrepRow<D>::PE;
 #pragma unroll
-        for (int m = 0; m < PE; ++m) {
-            const float angle = r.a[m] / r.f[m];
-            float sn, cs;
-            sincosf(angle, &sn, &cs);
-            const float p = r.x[m], q = r.x[m + PE];
-            r.x[m] = p * cs - q * sn;
-            r.x[m + PE] = p * sn + q * cs;
-        }
+    for (int m = 0; m < PE; ++m) {
+        const float c = cs[lane + 64 * m], s = sn[lane + 64 * m];
+        const float a = r.x[m], b = r.x[m + PE];
+        r.x[m] = a * c - b * s;
+        r.x[m + PE] = a * s + b * c;
     }
 }
 
