@@ -754,7 +754,10 @@ def main():
             "roofline": {"bound": "mfma", "achieved": round(c4["both_layers_tflops"], 2),
                          "peak": F32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(c4["frac_of_f32_mfma_peak"], 4),
-                         "traffic": None, "dtype": "f32 MFMA (v_mfma_f32_16x16x4f32)",
+                         "traffic": traffic_bytes("prefill_2048_sliding_and_global.txt"),
+                         "traffic_note": "HBM bytes of one step (both layers' prefill and merge launches) from "
+                                         "the rocprofv3 FETCH_SIZE / WRITE_SIZE passes in profiles/",
+                         "dtype": "f32 MFMA (v_mfma_f32_16x16x4f32)",
                          "mfma_busy_counter": {k2: v["mfma_busy"] for k2, v in mfma.items()} or None,
                          "mfma_source": "profiles/prefill_2048_sliding_and_global.txt (SQ_VALU_MFMA_BUSY_CYCLES)"},
             "cpu_baseline": cpu.get("4")},

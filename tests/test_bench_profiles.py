@@ -63,6 +63,9 @@ def test_prefill_summary_has_trace_and_mfma_busy():
         assert v.get("avg_us", 0) > 0
         busy = v.get("mfma_busy")
         assert busy is not None and 0.0 < busy < 1.0, (kernel, busy)
+    # HBM traffic of a step: MFMA-bound, so far below what the launches could stream
+    t = bench.traffic_bytes("prefill_2048_sliding_and_global.txt")
+    assert t is not None and 0 < t < 1e9, t
 
 
 def test_counter_calibration_factors():
