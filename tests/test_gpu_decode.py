@@ -42,6 +42,26 @@ def test_measured_decode_configs(ctx, name, T, d, glob):
     assert err <= TOL
 
 
+@pytest.mark.parametrize("T,d", [(131072, 512), (65536, 256)])
+def test_decode_longest_contexts(ctx, T, d):
+    """Gemma 4's longest context, one sequence: 256 splits of 512 keys (16
+    pairs per workgroup) on the global layer, and a whole-history d=256
+    cache of 64K rows; every row attended, against the oracle, and the
+    allocation-free form (its static scratch holds this plan) gives the same
+    bits."""
+    print(f"[case] decode T={T} d={d}", flush=True)
+    q, K, V, _ = I.decode_case(31 + T, T, d, d == 512)
+    out = run_decode(ctx, q, K, V, 0, T, 8, 1, d)
+    ref = orc.attend_rows(q, K, V, 8, 1, threads=8)  # bit-equal to attend (test_oracle), one head per thread
+    err = I.rel_err(out, ref)
+    print(f"[parity] decode T={T} d={d}: rel err {err:.2e}", flush=True)
+    assert err <= TOL
+    o2 = torch.zeros(8 * d, device="cuda")
+    ctx.attend_decode_noalloc(dev(q), dev(K), dev(V), 0, T, 8, 1, d, o2)
+    ctx.check_status()
+    assert np.array_equal(o2.cpu().numpy(), out)
+
+
 @pytest.mark.parametrize("d", [256, 512])
 @pytest.mark.parametrize("T", [1, 2, 15, 16, 17, 33, 100, 511, 512, 513, 1000])
 def test_decode_lengths(ctx, d, T):
