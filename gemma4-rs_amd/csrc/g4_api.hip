@@ -1221,7 +1221,9 @@ int g4_port_rope(g4_ctx *ctx, float *x, int64_t len, int64_t pos, float theta, i
         if (!ctx) return invalid("g4_port_rope: null context");
         if (dims <= 0 || dims % 2 != 0 || dims > len || theta <= 0.0f || pos < 0)
             return g4::set_error(G4_ERR_COMPUTE, "invalid RoPE inputs");
-        return g4_rope_neox_rows(ctx, x, 1, 1, (int)len, (int)dims, pos, theta, nullptr, 0, stream);
+        if (dims > INT32_MAX - 1) return invalid("g4_port_rope: dims above 2^31 - 2 are not supported");
+        // One row: values past dims are left alone, so the row is dims wide.
+        return g4_rope_neox_rows(ctx, x, 1, 1, (int)dims, (int)dims, pos, theta, nullptr, 0, stream);
     });
 }
 

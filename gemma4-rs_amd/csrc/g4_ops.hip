@@ -44,34 +44,45 @@ __global__ __launch_bounds__(256) void rms_norm_rows_kernel(const float *x, int6
 // rope_neox (ops.rs:134-162) on every head of one token per workgroup.  The
 // angle of pair i is theta_i / factor_i with theta_0 = position and
 // theta_{i+1} = theta_i * theta_scale in f32 -- a sequential recurrence, so
-// one lane builds the table and the workgroup applies it.
+// one lane builds the table and the workgroup applies it.  The table goes
+// through LDS kRopeChunk pairs at a time (the recurrence carried from one
+// chunk to the next), so any rotation width fits.
+constexpr int kRopeChunk = 4096;
+
 __global__ __launch_bounds__(256) void rope_rows_kernel(float *x, int n_heads, int head_dim,
                                                         int n_rot, int64_t pos0,
                                                         float theta_scale,
                                                         const float *factors) {
 #pragma clang fp contract(off)
-    extern __shared__ float theta[];  // [n_rot/2]
+    __shared__ float theta[kRopeChunk];
+    __shared__ float carry;
     const int half = n_rot / 2;
     const int64_t token = blockIdx.x;
-    if (threadIdx.x == 0) {
-        float t = (float)(pos0 + token);
-        for (int i = 0; i < half; ++i) {
-            theta[i] = t;
-            t = t * theta_scale;
-        }
-    }
-    __syncthreads();
     float *xt = x + token * (int64_t)n_heads * head_dim;
-    for (int e = threadIdx.x; e < n_heads * half; e += blockDim.x) {
-        const int h = e / half, i = e % half;
-        const float factor = factors ? factors[i] : 1.0f;
-        const float angle = theta[i] / factor;
-        float sn, cs;
-        sincosf(angle, &sn, &cs);
-        float *xh = xt + (int64_t)h * head_dim;
-        const float a = xh[i], b = xh[i + half];
-        xh[i] = a * cs - b * sn;
-        xh[i + half] = a * sn + b * cs;
+    if (threadIdx.x == 0) carry = (float)(pos0 + token);
+    for (int c0 = 0; c0 < half; c0 += kRopeChunk) {
+        const int len = min(kRopeChunk, half - c0);
+        __syncthreads();  // the previous chunk's readers are done with theta
+        if (threadIdx.x == 0) {
+            float t = carry;
+            for (int i = 0; i < len; ++i) {
+                theta[i] = t;
+                t = t * theta_scale;
+            }
+            carry = t;
+        }
+        __syncthreads();
+        for (int64_t e = threadIdx.x; e < (int64_t)n_heads * len; e += blockDim.x) {
+            const int h = (int)(e / len), j = (int)(e % len), i = c0 + j;
+            const float factor = factors ? factors[i] : 1.0f;
+            const float angle = theta[j] / factor;
+            float sn, cs;
+            sincosf(angle, &sn, &cs);
+            float *xh = xt + (int64_t)h * head_dim;
+            const float a = xh[i], b = xh[i + half];
+            xh[i] = a * cs - b * sn;
+            xh[i + half] = a * sn + b * cs;
+        }
     }
 }
 
@@ -312,9 +323,8 @@ int launch_rms_norm_rows(const float *x, int64_t n_rows, int64_t width, const fl
 int launch_rope_rows(float *x, int64_t n_tokens, int n_heads, int head_dim, int n_rot,
                      int64_t pos0, float theta_scale, const float *factors, hipStream_t stream) {
     if (n_tokens <= 0) return G4_OK;
-    hipLaunchKernelGGL(rope_rows_kernel, dim3((unsigned)n_tokens), dim3(256),
-                       (size_t)(n_rot / 2) * sizeof(float), stream, x, n_heads, head_dim, n_rot,
-                       pos0, theta_scale, factors);
+    hipLaunchKernelGGL(rope_rows_kernel, dim3((unsigned)n_tokens), dim3(256), 0, stream, x, n_heads,
+                       head_dim, n_rot, pos0, theta_scale, factors);
     G4_HIP(hipGetLastError());
     return G4_OK;
 }

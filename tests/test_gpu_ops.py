@@ -98,6 +98,20 @@ def test_rope_known_answers_and_errors(ctx):
         ctx.port_rope(t, 2, 1, 0.0, 2)
 
 
+@pytest.mark.parametrize("length,dims", [(50001, 40000), (8194, 8194)])
+def test_port_rope_wide_rows(ctx, length, dims):
+    """ComputePort::rope over rows wider than one LDS table chunk (4096
+    pairs): the angle recurrence carries across chunks, values past dims
+    stay as they were."""
+    x = np.random.default_rng(length).standard_normal(length).astype(np.float32)
+    t = dev(x)
+    ctx.port_rope(t, length, 12345, 10000.0, dims)
+    got = t.cpu().numpy()
+    ref = orc.rope_neox(x, 12345, 10000.0, dims)
+    assert np.max(np.abs(got - ref)) < 2e-5
+    assert np.array_equal(got[dims:], x[dims:])
+
+
 def test_compute_port_methods(ctx):
     """CpuPort's behaviour (crates/llm-backend-cpu/src/port.rs) on device buffers."""
     out = torch.zeros(4, device="cuda")
