@@ -166,7 +166,10 @@ __device__ __forceinline__ void prefill_unit(const PrefillK &p, const PrefillUni
     constexpr int TPS = S::TPS;
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    // The wavefront index is uniform; readfirstlane lets the compiler keep
+    // it, and the tile tests derived from it, in scalar registers and
+    // branch on them without exec masks.
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int rg = wave % kWaves;                           // row group
     const int half = S::SPLIT == 2 ? wave / kWaves : 0;     // dim half
     const int kpar = S::KSPLIT == 2 ? wave / kWaves : 0;    // tile parity
@@ -262,10 +265,13 @@ __device__ __forceinline__ void prefill_unit(const PrefillK &p, const PrefillUni
     // the wave group of parity j -- while the next step's tiles load into
     // (kn, vn).
     // Tile tt is in the unit and every row of the block attends all of its
-    // keys (key <= P0 and, with a window, key > P0 + 7 - W).
-    auto exact = [&](int tt) {
-        return tt < u.t_hi && 16LL * tt + 15 <= P0 && (win == 0 || 16LL * tt > P0 + kPosPerBlock - 1 - win);
-    };
+    // keys: 16 tt + 15 <= P0 and, with a window, 16 tt > P0 + 7 - W.  Those
+    // tiles are [ex_lo, ex_hi], found once per unit in 64 bits so that the
+    // per-step test is two 32-bit compares of tile indices.
+    const int ex_hi = (int)((P0 + 1) / 16 - 1);
+    const int64_t wlo = P0 + kPosPerBlock - 1 - win;
+    const int ex_lo = (win > 0 && wlo >= 0) ? (int)(wlo / 16 + 1) : 0;
+    auto exact = [&](int tt) { return tt < u.t_hi && tt >= ex_lo && tt <= ex_hi; };
     auto step = [&](int t, const f32x4 *kb, f32x4 *vb, f32x4 (*ls)[64], f32x4 *kn, f32x4 *vn) {
         // This step's tiles have landed (this wave's loads, then everyone's),
         // and every wave is done reading (kn, vn): fetch the next tiles into
