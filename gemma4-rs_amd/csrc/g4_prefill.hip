@@ -95,10 +95,12 @@ __device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 // Reductions over the four 16-lane rows of a wavefront (lanes c, c+16,
 // c+32, c+48), done with row swaps on the VALU and identical in every lane.
 __device__ inline float rows_max(float v) {
+    // NaN-propagating maximum: no operand canonicalisation (fmaxf needs it),
+    // and a NaN only shows up for a row already flagged non-finite.
     const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    const float h = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const float h = __builtin_elementwise_maximum(__uint_as_float(a[0]), __uint_as_float(a[1]));
     const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(h), __float_as_uint(h), false, false);
-    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+    return __builtin_elementwise_maximum(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 __device__ inline float rows_sum(float v) {
     const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
@@ -260,6 +262,7 @@ __device__ __forceinline__ void prefill_unit(const PrefillK &p, const PrefillUni
     for (int i = 0; i < NT; ++i) o[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     float m = -INFINITY, l = 0.0f;
     bool bad = false;
+    const bool scaled = p.scale != 1.0f;  // Gemma's scale is 1: x * 1 == x, skip the multiply
 
     // Tiles t .. t+TPS-1 are read from (kb, vb) -- tile t+j at j*TILE_F4, by
     // the wave group of parity j -- while the next step's tiles load into
@@ -356,7 +359,7 @@ __device__ __forceinline__ void prefill_unit(const PrefillK &p, const PrefillUni
         // pos - W.  Tiles every row of the block sees whole skip the test.
         float sv[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) sv[r] = sc[r] * p.scale;
+        for (int r = 0; r < 4; ++r) sv[r] = scaled ? sc[r] * p.scale : sc[r];
         const bool whole = exact(tw) || !live;  // a stale tile is masked whole below
         if (!live) {
 #pragma unroll
@@ -369,9 +372,13 @@ __device__ __forceinline__ void prefill_unit(const PrefillK &p, const PrefillUni
                 if (!(kr <= rel && (win == 0 || kr > rel - win))) sv[r] = -INFINITY;
             }
         }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) bad |= __builtin_amdgcn_classf(sv[r], 0x203);  // signalling/quiet NaN, +inf
-        const float mt = rows_max(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])));
+        // The lane's 4 scores (one row) by a NaN-propagating maximum
+        // (v_maximum3_f32): NaN or +inf among them shows in mx, so one class
+        // test flags the row.  For other scores mx is the plain maximum.
+        const float mx = __builtin_elementwise_maximum(__builtin_elementwise_maximum(sv[0], sv[1]),
+                                                       __builtin_elementwise_maximum(sv[2], sv[3]));
+        bad |= __builtin_amdgcn_classf(mx, 0x203);  // signalling/quiet NaN, +inf
+        const float mt = rows_max(mx);
         // Lazy rescaling: a row keeps its reference max m until a score
         // exceeds it by more than kRescaleSlack (p < 2^32 meanwhile, safe in
         // f32), so O is rescaled about once per row rather than every tile.

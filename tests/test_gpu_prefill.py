@@ -10,6 +10,7 @@ import numpy as np
 import pytest
 import torch
 
+import g4hip
 import inputs as I
 from oracle import pyoracle as orc
 
@@ -101,6 +102,34 @@ def test_prefill_non_finite_v_reaches_only_the_queries_that_attend_it(ctx, d, wi
     if window:
         for i in range(P0 - pos0 + 4, P0 - pos0 + 8):
             assert np.all(np.isfinite(got[i][np.concatenate([heads + 7, heads + 100])])), i
+
+
+@pytest.mark.parametrize("d,window", [(256, 512), (256, 16), (512, 0)])
+def test_prefill_non_finite_scores_fail_the_call(ctx, d, window):
+    """A NaN or +inf score (here from one K value) in a row that some query
+    attends fails the call with "softmax input is not finite", as that
+    query's softmax does in the token-at-a-time loop (model.rs:362-364,
+    ops.rs:116-121); a -inf score is only a zero weight.  q's dim 3 is made
+    positive so that an infinite K value there gives a score of its sign."""
+    pos0, N, row = 37, 45, 37 + 20
+    q, K, V = case(77 + d + window, pos0 + N, d, d == 512)
+    q = np.ascontiguousarray(q).copy()
+    q.reshape(pos0 + N, 8, d)[:, :, 3] = np.abs(q.reshape(pos0 + N, 8, d)[:, :, 3]) + 0.5
+    for name, value, fails in [("nan", np.nan, True), ("+inf", np.inf, True), ("-inf", -np.inf, False)]:
+        print(f"[case] prefill non-finite score {name} d={d} W={window}", flush=True)
+        Kx = K.copy()
+        Kx[row, 3] = value
+        ref, status = orc.attend_prefill(q[pos0:], Kx, V, pos0, window, 8, 1)
+        assert bool(status.any()) == fails, name
+        out = torch.zeros(N * 8 * d, device="cuda")
+        ctx.attend_prefill(dev(q[pos0:]), dev(Kx), dev(V), pos0, N, window, 8, 1, d, out)
+        if fails:
+            with pytest.raises(g4hip.EngError, match="softmax input is not finite"):
+                ctx.check_status()
+        else:
+            ctx.check_status()
+            check_all_rows(f"-inf score d={d} W={window}", out.cpu().numpy().reshape(N, 8 * d), q[pos0:], Kx, V,
+                           pos0, window)
 
 
 def test_prefill_never_reads_future_or_out_of_window_rows(ctx):
