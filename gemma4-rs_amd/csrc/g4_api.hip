@@ -191,6 +191,79 @@ int g4_release(g4_ctx *ctx) {
     });
 }
 
+// ------------------------------------------------------------ device memory
+int g4_alloc(g4_ctx *ctx, size_t bytes, void **ptr) {
+    return guarded([&] {
+        g4::clear_error();
+        if (!ctx || !ptr) return invalid("g4_alloc: null argument");
+        *ptr = nullptr;
+        if (bytes == 0) return (int)G4_OK;
+        G4_HIP(hipSetDevice(ctx->device));
+        G4_HIP(hipMalloc(ptr, bytes));
+        return (int)G4_OK;
+    });
+}
+
+int g4_free(g4_ctx *ctx, void *ptr) {
+    return guarded([&] {
+        g4::clear_error();
+        if (!ctx) return invalid("g4_free: null context");
+        if (!ptr) return (int)G4_OK;
+        G4_HIP(hipSetDevice(ctx->device));
+        G4_HIP(hipDeviceSynchronize());
+        G4_HIP(hipFree(ptr));
+        return (int)G4_OK;
+    });
+}
+
+namespace {
+
+int copy_sync(g4_ctx *ctx, void *dst, const void *src, size_t bytes, hipMemcpyKind kind, const char *name) {
+    return guarded([&] {
+        g4::clear_error();
+        if (!ctx) return invalid((std::string(name) + ": null context").c_str());
+        if (bytes == 0) return (int)G4_OK;
+        if (!dst || !src) return invalid((std::string(name) + ": null pointer").c_str());
+        G4_HIP(hipSetDevice(ctx->device));
+        G4_HIP(hipDeviceSynchronize());
+        G4_HIP(hipMemcpy(dst, src, bytes, kind));
+        return (int)G4_OK;
+    });
+}
+
+}  // namespace
+
+int g4_copy_to_device(g4_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    return copy_sync(ctx, dst, src, bytes, hipMemcpyHostToDevice, "g4_copy_to_device");
+}
+
+int g4_copy_to_host(g4_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    return copy_sync(ctx, dst, src, bytes, hipMemcpyDeviceToHost, "g4_copy_to_host");
+}
+
+int g4_copy_on_device(g4_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    return copy_sync(ctx, dst, src, bytes, hipMemcpyDeviceToDevice, "g4_copy_on_device");
+}
+
+int g4_sync(g4_ctx *ctx, g4_stream stream) {
+    return guarded([&] {
+        g4::clear_error();
+        if (!ctx) return invalid("g4_sync: null context");
+        G4_HIP(hipSetDevice(ctx->device));
+        G4_HIP(hipStreamSynchronize(as_stream(stream)));
+        return (int)G4_OK;
+    });
+}
+
+int g4_activate(g4_ctx *ctx) {
+    return guarded([&] {
+        g4::clear_error();
+        if (!ctx) return invalid("g4_activate: null context");
+        G4_HIP(hipSetDevice(ctx->device));
+        return (int)G4_OK;
+    });
+}
+
 int g4_check_status(g4_ctx *ctx, g4_stream stream) {
     return guarded([&] {
         if (!ctx) return invalid("g4_check_status: null context");

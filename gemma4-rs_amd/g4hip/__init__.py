@@ -56,6 +56,13 @@ _SIGS = {
     "g4_release": (c_int, [c_vp]),
     "g4_check_status": (c_int, [c_vp, c_vp]),
     "g4_set_decode_chunk": (c_int, [c_vp, c_i64]),
+    "g4_alloc": (c_int, [c_vp, c_size, ctypes.POINTER(c_vp)]),
+    "g4_free": (c_int, [c_vp, c_vp]),
+    "g4_copy_to_device": (c_int, [c_vp, c_vp, c_vp, c_size]),
+    "g4_copy_to_host": (c_int, [c_vp, c_vp, c_vp, c_size]),
+    "g4_copy_on_device": (c_int, [c_vp, c_vp, c_vp, c_size]),
+    "g4_sync": (c_int, [c_vp, c_vp]),
+    "g4_activate": (c_int, [c_vp]),
     "g4_attend": (c_int, [c_vp, c_vp, c_size, c_vp, c_vp, c_size, c_size, c_size, c_f32, c_vp]),
     "g4_attend_decode": (c_int, [c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_int, c_int, c_int, c_f32, c_vp, c_vp]),
     "g4_attend_decode_noalloc": (c_int, [c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_int, c_int, c_int, c_f32, c_vp,
@@ -152,6 +159,8 @@ def _ptr(t):
     """Device (or host) address of a torch tensor or numpy array, or None."""
     if t is None:
         return None
+    if isinstance(t, int):  # a raw address (Context.alloc)
+        return t
     if hasattr(t, "data_ptr"):
         return t.data_ptr()
     return t.ctypes.data
@@ -236,6 +245,31 @@ class Context:
 
     def set_decode_chunk(self, keys):
         _raise(lib().g4_set_decode_chunk(self.handle, keys))
+
+    # -- device memory (caller-owned buffers without torch) ----------------
+    def alloc(self, nbytes):
+        """A device address of nbytes on this context's device (None for 0)."""
+        ptr = c_vp()
+        _raise(lib().g4_alloc(self.handle, nbytes, ctypes.byref(ptr)))
+        return ptr.value
+
+    def free(self, ptr):
+        _raise(lib().g4_free(self.handle, ptr))
+
+    def copy_to_device(self, dst, src_host, nbytes):
+        _raise(lib().g4_copy_to_device(self.handle, dst, _ptr(src_host), nbytes))
+
+    def copy_to_host(self, dst_host, src, nbytes):
+        _raise(lib().g4_copy_to_host(self.handle, _ptr(dst_host), src, nbytes))
+
+    def copy_on_device(self, dst, src, nbytes):
+        _raise(lib().g4_copy_on_device(self.handle, dst, src, nbytes))
+
+    def sync(self, stream=None):
+        _raise(lib().g4_sync(self.handle, _stream(stream)))
+
+    def activate(self):
+        _raise(lib().g4_activate(self.handle))
 
     # -- attention ---------------------------------------------------------
     def attend(self, q, keys, values, n_heads, n_kv_heads, scale=1.0):

@@ -1,7 +1,7 @@
-//! Links libg4attn.so (`make -C gemma4-rs_amd`: hipcc --offload-arch=gfx950)
-//! and the HIP runtime it calls.  `G4ATTN_LIB_DIR` names the directory that
-//! holds the library (default: `../lib`, beside this crate in gemma4-rs_amd);
-//! `ROCM_PATH` the ROCm install (default /opt/rocm).
+//! Links libg4attn.so (`make -C gemma4-rs_amd`: hipcc --offload-arch=gfx950),
+//! the only library the crate binds; it brings the HIP runtime in itself.
+//! `G4ATTN_LIB_DIR` names the directory that holds it (default: `../lib`,
+//! beside this crate in gemma4-rs_amd).
 
 use std::env;
 use std::path::PathBuf;
@@ -11,14 +11,10 @@ fn main() {
     let lib_dir = env::var("G4ATTN_LIB_DIR")
         .map(PathBuf::from)
         .unwrap_or_else(|_| manifest.join("..").join("lib"));
-    let rocm = env::var("ROCM_PATH").unwrap_or_else(|_| "/opt/rocm".to_owned());
     println!("cargo:rustc-link-search=native={}", lib_dir.display());
-    println!("cargo:rustc-link-search=native={rocm}/lib");
     println!("cargo:rustc-link-lib=dylib=g4attn");
-    println!("cargo:rustc-link-lib=dylib=amdhip64");
     // Binaries and tests find the library where it was linked from.
     println!("cargo:rustc-link-arg=-Wl,-rpath,{}", lib_dir.display());
     println!("cargo:rerun-if-env-changed=G4ATTN_LIB_DIR");
-    println!("cargo:rerun-if-env-changed=ROCM_PATH");
     println!("cargo:rerun-if-changed=build.rs");
 }

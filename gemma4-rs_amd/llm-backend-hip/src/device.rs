@@ -5,11 +5,11 @@ use std::fmt;
 use std::marker::PhantomData;
 use std::mem::size_of;
 use std::ptr;
-use std::sync::{Mutex, PoisonError};
+use std::sync::{Arc, Mutex, PoisonError};
 
 use llm_eng::EngError;
 
-use crate::error::{check, hip};
+use crate::error::check;
 use crate::ffi;
 
 /// One `g4_ctx`: a device's split-K workspace and softmax status word.
@@ -39,18 +39,18 @@ impl Context {
         self.device
     }
 
-    /// Makes the context's device current on the calling thread (where
-    /// `DeviceVec` allocations go).
+    /// Makes the context's device the calling thread's current HIP device
+    /// (`g4_activate`), for the device-pointer calls that run on it.
     pub fn activate(&self) -> Result<(), EngError> {
-        // SAFETY: plain runtime call.
-        hip(unsafe { ffi::hipSetDevice(self.device) }, "hipSetDevice")
+        // SAFETY: the context is live.
+        self.call(|c| unsafe { ffi::g4_activate(c) })
     }
 
-    /// Runs one C entry point with the raw context, under the lock and on
-    /// the context's device, and maps its status.
+    /// Runs one C entry point with the raw context, under the lock, and
+    /// maps its status.  (Entry points that allocate or copy make the
+    /// context's device current themselves.)
     pub(crate) fn call(&self, f: impl FnOnce(*mut ffi::G4Ctx) -> c_int) -> Result<(), EngError> {
         let guard = self.raw.lock().unwrap_or_else(PoisonError::into_inner);
-        self.activate()?;
         check(f(guard.0))
     }
 }
@@ -90,12 +90,6 @@ impl Stream {
     pub fn as_raw(self) -> *mut c_void {
         self.0
     }
-
-    /// `hipStreamSynchronize`.
-    pub fn synchronize(self) -> Result<(), EngError> {
-        // SAFETY: self.0 is null or a valid stream (from_raw's contract).
-        hip(unsafe { ffi::hipStreamSynchronize(self.0) }, "hipStreamSynchronize")
-    }
 }
 
 impl Default for Stream {
@@ -104,11 +98,13 @@ impl Default for Stream {
     }
 }
 
-/// An owned device allocation of `len` values of `T` (hipMalloc on the
-/// current device, hipFree on drop).  Zero-length buffers allocate nothing.
+/// An owned device allocation of `len` values of `T` on a context's device
+/// (`g4_alloc`, freed by `g4_free` on drop).  Zero-length buffers allocate
+/// nothing.
 pub struct DeviceVec<T: Copy> {
     ptr: *mut T,
     len: usize,
+    ctx: Arc<Context>,
     _owns: PhantomData<T>,
 }
 
@@ -123,27 +119,25 @@ unsafe impl<T: Copy + Sync> Sync for DeviceVec<T> {}
 
 impl<T: Copy> DeviceVec<T> {
     /// `len` values whose contents are whatever the allocation held.
-    pub fn uninit(len: usize) -> Result<Self, EngError> {
+    pub fn uninit(ctx: &Arc<Context>, len: usize) -> Result<Self, EngError> {
         let bytes = len
             .checked_mul(size_of::<T>())
             .ok_or_else(|| EngError::Msg(format!("a device buffer of {len} values overflows usize")))?;
         let mut raw: *mut c_void = ptr::null_mut();
-        if bytes > 0 {
-            // SAFETY: raw is a valid out-pointer.
-            hip(unsafe { ffi::hipMalloc(&mut raw, bytes) }, "hipMalloc")?;
-        }
-        Ok(Self { ptr: raw.cast(), len, _owns: PhantomData })
+        let out: *mut *mut c_void = &mut raw;
+        // SAFETY: out is a valid out-pointer.
+        ctx.call(|c| unsafe { ffi::g4_alloc(c, bytes, out) })?;
+        Ok(Self { ptr: raw.cast(), len, ctx: Arc::clone(ctx), _owns: PhantomData })
     }
 
     /// A device copy of `values` (synchronous).
-    pub fn from_slice(values: &[T]) -> Result<Self, EngError> {
-        let mut buf = Self::uninit(values.len())?;
+    pub fn from_slice(ctx: &Arc<Context>, values: &[T]) -> Result<Self, EngError> {
+        let mut buf = Self::uninit(ctx, values.len())?;
         buf.copy_from_slice(values)?;
         Ok(buf)
     }
 
-    /// Overwrites the buffer with `values` (synchronous; ordered after the
-    /// null stream's work).
+    /// Overwrites the buffer with `values`, after the device's queued work.
     pub fn copy_from_slice(&mut self, values: &[T]) -> Result<(), EngError> {
         if values.len() != self.len {
             return Err(EngError::Msg(format!(
@@ -152,58 +146,28 @@ impl<T: Copy> DeviceVec<T> {
                 self.len
             )));
         }
-        if self.len > 0 {
-            // SAFETY: source and destination both hold self.bytes() bytes.
-            hip(
-                unsafe {
-                    ffi::hipMemcpy(self.ptr.cast(), values.as_ptr().cast(), self.bytes(), ffi::HIP_MEMCPY_HOST_TO_DEVICE)
-                },
-                "hipMemcpy",
-            )?;
-        }
-        Ok(())
+        let (dst, src, bytes) = (self.ptr.cast::<c_void>(), values.as_ptr().cast::<c_void>(), self.bytes());
+        // SAFETY: source and destination both hold `bytes` bytes.
+        self.ctx.call(|c| unsafe { ffi::g4_copy_to_device(c, dst, src, bytes) })
     }
 
-    /// The values on the host (synchronous; ordered after the null stream's
-    /// work -- synchronize another stream first).
+    /// The values on the host, after the device's queued work.
     pub fn to_vec(&self) -> Result<Vec<T>, EngError> {
         let mut out = Vec::<T>::with_capacity(self.len);
-        if self.len > 0 {
-            // SAFETY: out has room for self.len values, all written by the copy
-            // before set_len.
-            unsafe {
-                hip(
-                    ffi::hipMemcpy(
-                        out.as_mut_ptr().cast(),
-                        self.ptr.cast_const().cast(),
-                        self.bytes(),
-                        ffi::HIP_MEMCPY_DEVICE_TO_HOST,
-                    ),
-                    "hipMemcpy",
-                )?;
-                out.set_len(self.len);
-            }
-        }
+        let (dst, src, bytes) = (out.as_mut_ptr().cast::<c_void>(), self.ptr.cast_const().cast::<c_void>(), self.bytes());
+        // SAFETY: out has room for self.len values; the copy writes all of
+        // them before set_len.
+        self.ctx.call(|c| unsafe { ffi::g4_copy_to_host(c, dst, src, bytes) })?;
+        unsafe { out.set_len(self.len) };
         Ok(out)
     }
 
     /// A second device buffer with the same values (synchronous).
     pub fn try_clone(&self) -> Result<Self, EngError> {
-        let copy = Self::uninit(self.len)?;
-        if self.len > 0 {
-            // SAFETY: both allocations hold self.bytes() bytes.
-            hip(
-                unsafe {
-                    ffi::hipMemcpy(
-                        copy.ptr.cast(),
-                        self.ptr.cast_const().cast(),
-                        self.bytes(),
-                        ffi::HIP_MEMCPY_DEVICE_TO_DEVICE,
-                    )
-                },
-                "hipMemcpy",
-            )?;
-        }
+        let copy = Self::uninit(&self.ctx, self.len)?;
+        let (dst, src, bytes) = (copy.ptr.cast::<c_void>(), self.ptr.cast_const().cast::<c_void>(), self.bytes());
+        // SAFETY: both allocations hold `bytes` bytes.
+        self.ctx.call(|c| unsafe { ffi::g4_copy_on_device(c, dst, src, bytes) })?;
         Ok(copy)
     }
 
@@ -224,6 +188,11 @@ impl<T: Copy> DeviceVec<T> {
         self.ptr
     }
 
+    /// The context the buffer was allocated on.
+    pub fn context(&self) -> &Arc<Context> {
+        &self.ctx
+    }
+
     fn bytes(&self) -> usize {
         self.len * size_of::<T>()
     }
@@ -232,9 +201,10 @@ impl<T: Copy> DeviceVec<T> {
 impl<T: Copy> Drop for DeviceVec<T> {
     fn drop(&mut self) {
         if !self.ptr.is_null() {
-            // SAFETY: ptr came from hipMalloc and is freed once; hipFree waits
-            // for the device work that may still use it.
-            unsafe { ffi::hipFree(self.ptr.cast()) };
+            let p = self.ptr.cast::<c_void>();
+            // SAFETY: p came from g4_alloc on this context and is freed once;
+            // g4_free waits for the device work that may still use it.
+            let _ = self.ctx.call(|c| unsafe { ffi::g4_free(c, p) });
         }
     }
 }

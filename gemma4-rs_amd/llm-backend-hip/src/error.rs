@@ -30,16 +30,6 @@ pub fn check(code: c_int) -> Result<(), EngError> {
     })
 }
 
-/// `hipError_t` -> `Result`, naming the runtime call that failed.
-pub fn hip(error: ffi::HipError, call: &str) -> Result<(), EngError> {
-    if error == ffi::HIP_SUCCESS {
-        return Ok(());
-    }
-    // SAFETY: hipGetErrorString returns a static NUL-terminated string.
-    let name = unsafe { CStr::from_ptr(ffi::hipGetErrorString(error)) }.to_string_lossy().into_owned();
-    Err(EngError::Compute(format!("hip: {name} ({call})")))
-}
-
 /// The CPU backend's `compute_error` (crates/llm-backend-cpu/src/ops.rs:5-7).
 pub(crate) fn compute_error(message: impl Into<String>) -> EngError {
     EngError::Compute(message.into())

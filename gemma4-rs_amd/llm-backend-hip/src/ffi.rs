@@ -1,8 +1,9 @@
-//! Raw declarations: every function of `include/g4attn.h` (the C ABI of
-//! `libg4attn.so`), and the HIP runtime calls the safe wrappers use for
-//! device memory.  Parameter names follow the header (lower-cased); the
-//! types map `int` -> `c_int`, `int64_t` -> `i64`, `size_t` -> `usize`,
-//! `g4_stream` -> `*mut c_void` (a `hipStream_t`, null for the null stream).
+//! Raw declarations: every function of `include/g4attn.h`, the C ABI of
+//! `libg4attn.so` -- the only library the crate binds (device memory
+//! included: `g4_alloc`, `g4_copy_*`, `g4_free`).  Parameter names follow the
+//! header (lower-cased); the types map `int` -> `c_int`, `int64_t` -> `i64`,
+//! `size_t` -> `usize`, `g4_stream` -> `*mut c_void` (a `hipStream_t`, null
+//! for the null stream).
 
 use std::ffi::{c_char, c_int, c_void};
 
@@ -51,6 +52,28 @@ extern "C" {
     pub fn g4_release(ctx: *mut G4Ctx) -> c_int;
     pub fn g4_check_status(ctx: *mut G4Ctx, stream: *mut c_void) -> c_int;
     pub fn g4_set_decode_chunk(ctx: *mut G4Ctx, keys: i64) -> c_int;
+    pub fn g4_alloc(ctx: *mut G4Ctx, bytes: usize, ptr_dev: *mut *mut c_void) -> c_int;
+    pub fn g4_free(ctx: *mut G4Ctx, ptr_dev: *mut c_void) -> c_int;
+    pub fn g4_copy_to_device(
+        ctx: *mut G4Ctx,
+        dst_dev: *mut c_void,
+        src_host: *const c_void,
+        bytes: usize,
+    ) -> c_int;
+    pub fn g4_copy_to_host(
+        ctx: *mut G4Ctx,
+        dst_host: *mut c_void,
+        src_dev: *const c_void,
+        bytes: usize,
+    ) -> c_int;
+    pub fn g4_copy_on_device(
+        ctx: *mut G4Ctx,
+        dst_dev: *mut c_void,
+        src_dev: *const c_void,
+        bytes: usize,
+    ) -> c_int;
+    pub fn g4_sync(ctx: *mut G4Ctx, stream: *mut c_void) -> c_int;
+    pub fn g4_activate(ctx: *mut G4Ctx) -> c_int;
     pub fn g4_attend(
         ctx: *mut G4Ctx,
         q_host: *const f32,
@@ -452,21 +475,4 @@ extern "C" {
         out_dev: *mut f32,
         stream: *mut c_void,
     ) -> c_int;
-}
-
-/// `hipError_t`; 0 is `hipSuccess`.
-pub type HipError = c_int;
-pub const HIP_SUCCESS: HipError = 0;
-/// `hipMemcpyKind` values.
-pub const HIP_MEMCPY_HOST_TO_DEVICE: c_int = 1;
-pub const HIP_MEMCPY_DEVICE_TO_HOST: c_int = 2;
-pub const HIP_MEMCPY_DEVICE_TO_DEVICE: c_int = 3;
-
-extern "C" {
-    pub fn hipSetDevice(device: c_int) -> HipError;
-    pub fn hipMalloc(ptr: *mut *mut c_void, size: usize) -> HipError;
-    pub fn hipFree(ptr: *mut c_void) -> HipError;
-    pub fn hipMemcpy(dst: *mut c_void, src: *const c_void, size: usize, kind: c_int) -> HipError;
-    pub fn hipStreamSynchronize(stream: *mut c_void) -> HipError;
-    pub fn hipGetErrorString(error: HipError) -> *const c_char;
 }

@@ -14,9 +14,10 @@
 //! - Mat-vecs ([`matvec`]) over GGUF weight blobs uploaded once.
 //!
 //! Errors are `EngError` with the reference's variants and texts; the
-//! status codes of the C side map back in [`error::check`].  Every
-//! declaration of `ffi` is checked against the header by
-//! tests/test_rust_binding.py.
+//! status codes of the C side map back in [`error::check`].  Device memory
+//! comes from the library too (`g4_alloc`, `g4_copy_*`, `g4_free`), so the
+//! crate binds `libg4attn.so` alone.  Every declaration of `ffi` is checked
+//! against the header by tests/test_rust_binding.py.
 
 pub mod attention;
 pub mod device;

@@ -27,7 +27,7 @@ impl HipPort {
     pub fn quantize_q8_0(&self, x: &DevBuf) -> Result<DeviceQ8, EngError> {
         let n = len_i64(x.len())?;
         let mut scales = self.alloc(x.len() / 32)?;
-        let mut quants = DeviceVec::<i8>::uninit(x.len())?;
+        let mut quants = DeviceVec::<i8>::uninit(self.context(), x.len())?;
         let (px, ps, pq, stream) = (x.as_ptr(), scales.as_mut_ptr(), quants.as_mut_ptr(), self.stream().as_raw());
         // SAFETY: x holds n floats, scales n/32 and quants n (a length that is
         // not a multiple of 32 is rejected before any access).

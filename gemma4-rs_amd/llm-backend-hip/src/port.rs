@@ -46,13 +46,14 @@ impl HipPort {
 
     /// `F32Buf::from(values)` on the device (synchronous).
     pub fn upload(&self, values: &[f32]) -> Result<DevBuf, EngError> {
-        self.ctx.activate()?;
-        DevBuf::from_slice(values)
+        DevBuf::from_slice(&self.ctx, values)
     }
 
     /// The buffer's values once the port's queued work is done.
     pub fn download(&self, buf: &DevBuf) -> Result<Vec<f32>, EngError> {
-        self.stream.synchronize()?;
+        let stream = self.stream.as_raw();
+        // SAFETY: ctx is live; stream is null or valid (Stream::from_raw).
+        self.ctx.call(|ctx| unsafe { ffi::g4_sync(ctx, stream) })?;
         buf.to_vec()
     }
 
@@ -66,8 +67,7 @@ impl HipPort {
 
     /// An output buffer of `len` values on the port's device.
     pub(crate) fn alloc(&self, len: usize) -> Result<DevBuf, EngError> {
-        self.ctx.activate()?;
-        DevBuf::uninit(len)
+        DevBuf::uninit(&self.ctx, len)
     }
 }
 

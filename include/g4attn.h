@@ -65,6 +65,28 @@ int g4_check_status(g4_ctx *ctx, g4_stream stream);
 /* Tuning: keys per split-K work item of the decode kernels (0 = automatic). */
 int g4_set_decode_chunk(g4_ctx *ctx, int64_t keys);
 
+/* ---------------------------------------------------------- device memory */
+/* Caller-owned device buffers on the context's device, so that a binding
+ * needs no other runtime: the device image of F32Buf
+ * (crates/llm-backend-cpu/src/buffer.rs:1-26) and of the GGUF weight blobs
+ * the mat-vecs read (crates/llm-eng/src/weight_store.rs:5-22).  The library
+ * keeps no hidden copy of them.  0 bytes gives NULL. */
+int g4_alloc(g4_ctx *ctx, size_t bytes, void **ptr_dev);
+/* Frees a g4_alloc buffer after the device's queued work (NULL: no-op). */
+int g4_free(g4_ctx *ctx, void *ptr_dev);
+/* Synchronous copies of `bytes`, after all work queued on the device: host
+ * to device, device to host, device to device. */
+int g4_copy_to_device(g4_ctx *ctx, void *dst_dev, const void *src_host, size_t bytes);
+int g4_copy_to_host(g4_ctx *ctx, void *dst_host, const void *src_dev, size_t bytes);
+int g4_copy_on_device(g4_ctx *ctx, void *dst_dev, const void *src_dev, size_t bytes);
+/* Waits for `stream` (NULL: the null stream).  g4_check_status waits too,
+ * and also reports softmax failures. */
+int g4_sync(g4_ctx *ctx, g4_stream stream);
+/* Makes the context's device the calling thread's current HIP device.  The
+ * device-pointer calls below run on the current device, as HIP calls do;
+ * g4_init, g4_alloc, g4_copy_* and g4_sync make it current themselves. */
+int g4_activate(g4_ctx *ctx);
+
 /* ------------------------------------------------------ attention (hot path) */
 /* attend (model.rs:348-366), host buffers: q[n_heads*head_dim] with
  * head_dim = q_len / n_heads, keys/values [T][n_kv_heads*head_dim] (the
