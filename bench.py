@@ -17,7 +17,7 @@ MI355X's 8 TB/s; `cpu_baseline` is the oracle (the C restatement of the
 reference's CPU attention with its `concat` copy and per-head thread pool)
 running the reference's per-sequence loop on this host's cores.
 
-`configs` carries each of the five configurations with its own roofline and
+`configs` carries each measured workload, keyed in this order, with its own roofline and
 CPU baseline: 1 sliding decode over 64 keys, 2 global decode over 4096 keys
 (HBM-cold: K/V copies rotated), 3 the 35-layer E2B stack at context 8192
 (cold and resident), 4 a 2048-token prefill through a sliding and a global
@@ -124,7 +124,7 @@ def time_steps(torch, fn, steps, warmup):
 
 # ----------------------------------------------------------------- GPU side
 def bench_sliding_decode(ctx, torch, prep, steps, warmup, T=64, d=256):
-    """Configuration 1: one sliding-layer decode over 64 keys (147 KB; its
+    """One sliding-layer decode over 64 keys (147 KB; its
     rows stay cached between steps: a launch-latency figure)."""
     K = prep.rows(T, d, 0, LOCAL_BASE, None)
     V = prep.rows(T, d, 0, 0.0, None, rope=False)
@@ -138,7 +138,7 @@ def bench_sliding_decode(ctx, torch, prep, steps, warmup, T=64, d=256):
 
 
 def bench_global_decode(ctx, torch, prep, steps, warmup, T=4096, d=512):
-    """Configuration 2: one global-layer decode over 4096 keys.  Each step
+    """One global-layer decode over 4096 keys.  Each step
     reads one of `copies` K/V copies (more than 1.5x the 256 MB Infinity
     Cache between two reads of a copy), so its K/V come from HBM; the same
     step on one resident copy is reported beside it."""
@@ -180,7 +180,7 @@ def stack_plan(g4hip, ctx_len):
 
 
 def bench_stack(ctx, torch, prep, g4hip, steps, warmup, ctx_len=8192, cold=True, want_host=False):
-    """Configuration 3: the 35-layer E2B stack, one decode step at position
+    """The 35-layer E2B stack, one decode step at position
     ctx_len - 1: each layer's attention over its source layer's cache
     (owners 0..14, layers 15..34 reading 13/14), one call per layer.  Cold:
     the 15 owners' caches exist in `copies` copies, one per step in turn, so
@@ -223,7 +223,7 @@ def bench_stack(ctx, torch, prep, g4hip, steps, warmup, ctx_len=8192, cold=True,
 
 
 def bench_prefill(ctx, torch, prep, steps, warmup, N=2048, want_host=False):
-    """Configuration 4: a causal prefill of an N-token prompt through one
+    """A causal prefill of an N-token prompt through one
     sliding and one global layer.  All timed steps replay as one captured
     graph after at least 50 untimed steps: the clocks need tens of
     milliseconds of this load to settle (global layer 348 us after 2 warm-up
@@ -257,7 +257,7 @@ def bench_prefill(ctx, torch, prep, steps, warmup, N=2048, want_host=False):
 
 
 def bench_ragged(ctx, torch, prep, steps, warmup, want_host=False):
-    """Configuration 5: the ragged batch, global layer (whole contexts,
+    """The ragged batch of 32 sequences, global layer (whole contexts,
     2.04 GB of K/V, larger than the Infinity Cache: HBM-cold by size) and
     sliding layer (the last 512 rows of each sequence, 34 MB: resident
     between steps).  Timed per layer and as the whole step (both layers)."""
@@ -563,7 +563,7 @@ def cpu_decode(cpu, host, T, nbytes, seconds):
 
 
 def cpu_stack(cpu, host, nbytes, seconds):
-    """Configuration 3: the reference's layer loop, one attend per layer
+    """The E2B stack on the CPU: the reference's layer loop, one attend per layer
     over its source layer's rows (model.rs:407-410)."""
     import numpy as np
     rows = {l: cpu.rows(K, V) for l, (K, V) in host["kv"].items()}
@@ -582,7 +582,7 @@ def cpu_stack(cpu, host, nbytes, seconds):
 
 
 def cpu_prefill(cpu, host, seconds, stride=8):
-    """Configuration 4: the reference's prompt loop, one attend per token
+    """Prefill on the CPU: the reference's prompt loop, one attend per token
     (crates/llm-gemma4/src/impl_/generate.rs:37-41), on every `stride`-th
     position of the 2048-token prompt; TFLOP/s from the sampled positions'
     own FLOPs."""
@@ -613,7 +613,7 @@ def cpu_prefill(cpu, host, seconds, stride=8):
 
 
 def cpu_ragged(cpu, host, nbytes, seconds):
-    """Configuration 5: the reference's engine is single-sequence, so the
+    """The ragged batch on the CPU: the reference's engine is single-sequence, so the
     batch is a loop over the 32 sequences, one attend each per layer."""
     import numpy as np
     lens = host["lens"]
@@ -709,7 +709,7 @@ def main():
     for r in (c1, c2, c3w, c4, c5):
         r.pop("host", None)
 
-    # The headline: configuration 5, both layers per step.
+    # The headline: the ragged batch of 32 sequences, both layers per step.
     step_s = c5["step"]["us"] * 1e-6
     g5 = c5["global_d512"]
     prof5 = "decode_ragged_b32_ctx1k-32k.txt"

@@ -27,9 +27,9 @@ def run_decode(ctx, q, K, V, begin, end, n_heads, n_kv, d, scale=1.0):
     return out.cpu().numpy()
 
 
-@pytest.mark.parametrize("name,T,d,glob", [("config1_sliding_ctx64", 64, 256, False),
-                                           ("config2_global_ctx4096", 4096, 512, True)])
-def test_measured_decode_configs(ctx, name, T, d, glob):
+@pytest.mark.parametrize("name,T,d,glob", [("sliding_d256_ctx64", 64, 256, False),
+                                           ("global_d512_ctx4096", 4096, 512, True)])
+def test_measured_decode_workloads(ctx, name, T, d, glob):
     print(f"[case] {name}", flush=True)
     q, K, V, _ = I.decode_case(1000 + T, T, d, glob)
     begin, end = I.attended_range(T - 1, 0 if glob else I.WINDOW)
@@ -175,8 +175,8 @@ def test_empty_context_is_an_error(ctx):
 
 
 @pytest.mark.parametrize("d,glob", [(512, True), (256, False)])
-def test_ragged_batch_config5(ctx, d, glob):
-    """32 sequences, lengths U[1024, 32768], one launch (configuration 5)."""
+def test_ragged_batch_32_sequences_1k_to_32k(ctx, d, glob):
+    """32 sequences, lengths U[1024, 32768], one launch per layer type."""
     print(f"[case] ragged batch d={d}", flush=True)
     lens = I.ragged_lengths(2024)
     B = lens.size

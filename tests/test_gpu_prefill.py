@@ -64,8 +64,8 @@ def check_all_rows(name, got, q, K, V, pos0, window):
     return worst
 
 
-@pytest.mark.parametrize("name,d,window", [("config4_sliding_W512", 256, 512), ("config4_global", 512, 0)])
-def test_config4_prefill_2048(ctx, name, d, window):
+@pytest.mark.parametrize("name,d,window", [("sliding_d256_W512", 256, 512), ("global_d512", 512, 0)])
+def test_prefill_2048_every_row(ctx, name, d, window):
     """2048-token prompt: every query row against the oracle."""
     print(f"[case] {name}", flush=True)
     N = 2048

@@ -85,12 +85,12 @@ def test_synthetic_model_shape_generation(ctx):
     assert worst <= TOL
 
 
-def test_config3_e2b_stack_decode_at_8192(ctx):
-    """Configuration 3: 35 layers, owners hold 8191 rows, one decode step at
+def test_e2b_stack_decode_at_8192(ctx):
+    """The E2B stack: 35 layers, owners hold 8191 rows, one decode step at
     position 8191 through every layer (shared layers read 13 / 14)."""
-    print("[case] config3 E2B stack ctx 8192", flush=True)
+    print("[case] E2B stack ctx 8192", flush=True)
     worst = run_stack(ctx, g4hip.G4Hparams.e2b(), orc.Hparams.e2b(), 8191, [8191], 77)
-    print(f"[parity] config3: worst rel err {worst:.2e}")
+    print(f"[parity] E2B stack: worst rel err {worst:.2e}")
     assert worst <= TOL
 
 
