@@ -13,7 +13,8 @@ fn main() {
         .unwrap_or_else(|_| manifest.join("..").join("lib"));
     println!("cargo:rustc-link-search=native={}", lib_dir.display());
     println!("cargo:rustc-link-lib=dylib=g4attn");
-    // Binaries and tests find the library where it was linked from.
+    // This package's test binaries find the library where it was linked
+    // from; Cargo does not pass link arguments on to dependent crates.
     println!("cargo:rustc-link-arg=-Wl,-rpath,{}", lib_dir.display());
     println!("cargo:rerun-if-env-changed=G4ATTN_LIB_DIR");
     println!("cargo:rerun-if-changed=build.rs");
