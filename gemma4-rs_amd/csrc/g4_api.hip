@@ -286,6 +286,13 @@ int g4_set_decode_chunk(g4_ctx *ctx, int64_t keys) {
     return G4_OK;
 }
 
+int g4_set_prefill_exact(g4_ctx *ctx, int exact) {
+    if (!ctx) return invalid("g4_set_prefill_exact: null context");
+    if (exact != 0 && exact != 1) return invalid("g4_set_prefill_exact: exact must be 0 or 1");
+    ctx->prefill_exact = exact;
+    return G4_OK;
+}
+
 // ------------------------------------------------------------------ attention
 static int check_heads(int n_heads, int n_kv_heads, int head_dim) {
     if (n_heads <= 0 || n_kv_heads <= 0 || head_dim <= 0)
@@ -399,6 +406,8 @@ int attend_prefill_rows(g4_ctx *ctx, const float *q, const float *k_cache, const
     int rc = check_heads(n_heads, n_kv_heads, head_dim);
     if (rc != G4_OK) return rc;
     if (row_stride < (int64_t)n_kv_heads * head_dim) return invalid("row_stride below the row width");
+    const int64_t first_row = (window > 0 && pos0 + 1 > window) ? pos0 + 1 - window : 0;
+    if (kv_origin < 0 || kv_origin > first_row) return invalid("prefill attends rows before the first row held");
     g4::PrefillArgs a{};
     a.q = q;
     a.k = k_cache;

@@ -42,6 +42,7 @@ struct g4_ctx {
     unsigned *status_dev = nullptr;  // kStatus* bits, cleared by g4_check_status
     g4::Workspace ws;                // split-K partials of the decode kernels
     int64_t decode_chunk = 0;        // 0 = automatic
+    int prefill_exact = 0;           // 1: prefill uses f32 MFMAs only (no split-f16 products)
     int num_cus = 256;
     int64_t *zero_rows = nullptr;    // device zeros: default row offsets of a batch
     int64_t zero_rows_len = 0;

@@ -25,6 +25,7 @@
 // merge kernel combines them in key order.
 
 #include <algorithm>
+#include <cmath>
 #include <array>
 #include <functional>
 #include <queue>
@@ -59,6 +60,51 @@ constexpr int kPrefillMaxUnitsDev = 8;  // partial units per block (merge weight
 // GPUs, gfx950 included.
 constexpr int kBufferWord3 = 0x00020000;
 
+// Split-f16 products.  An f32 value x is carried as two f16 values, hi =
+// rn16(x) and lo = rn16((x - hi) * 2^11) (x - hi is exact in f32), so x =
+// hi + lo * 2^-11 to within max(2^-22 |x|, 2^-36): the scaled lo keeps the
+// residue of a small x out of the f16 subnormals (Ootomo & Yokota,
+// "Recovering single precision accuracy from Tensor Cores while surpassing
+// the FP32 theoretical peak performance", IJHPCA 2022, in its f16 form).  A
+// score q.k is then hi.hi' + 2^-11 (hi.lo' + lo.hi') -- three
+// v_mfma_f32_16x16x32_f16 into f32 accumulators, the two corrections in
+// their own -- at 16x the f32 MFMA's products per instruction, so 3/16 of
+// its matrix cycles; the dropped lo.lo' term is below 2^-22 |q_d k_d|.
+// The f16 MFMAs keep subnormal operands and form products exactly.
+//
+// P.V splits V the same way without the scale (V's residue error, at most
+// 2^-25 per element, is weighted by p/l <= 1) and carries the weights
+// scaled by 2^kPScale instead: with the rescale slack below they stay under
+// 2^15, and a weight's own floor is 2^-25 / 2^kPScale = 2^-32 of the row's
+// reference weight, which keeps large |v| from amplifying it.
+//
+// hi stays finite for |x| < 2^15; a unit whose q rows or K/V tiles hold
+// anything else (a larger value, NaN, inf) runs with f32 MFMAs instead,
+// which also keeps the reference's non-finite semantics.
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+constexpr float kSplitMax = 32768.0f;
+constexpr float kLoScale = 2048.0f, kLoUnscale = 1.0f / 2048.0f;  // 2^11
+// Weights p = 2^kPScale e^(s - m) with a slack of 8 log2 units stay below
+// 2^15 (finite in f16).  Partials report m - kPScale ln 2, so that their
+// (m, l, O) mean the same as the f32 form's.
+constexpr int kPScale = 7;
+constexpr float kRescaleSlackSplit = 8.0f / 1.4426950408889634f;
+constexpr float kPScaleNat = 7.0f * 0.6931471805599453f;
+
+__device__ inline f32x4 split_mfma(f16x8 a, f16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// hi and lo halves of x, lo unscaled (V) or scaled by 2^11 (Q, K); `bad` is
+// raised for a value the split does not carry.
+template <bool SCALED>
+__device__ inline void split_f16(float x, _Float16 &hi, _Float16 &lo, bool &bad) {
+    bad |= !(__builtin_fabsf(x) < kSplitMax);  // NaN compares false
+    hi = (_Float16)x;
+    const float r = x - (float)hi;
+    lo = (_Float16)(SCALED ? r * kLoScale : r);
+}
+
 struct PrefillUnit {
     int block;   // position block: positions pos0 + 8*block .. +7
     int t_lo;    // first 16-key tile
@@ -88,7 +134,103 @@ struct PrefillK {
     float2 *part_ml;  // [slot][kv head][64 rows]
     int n_slots;
     unsigned *status;
+    // Split-f16 planes of K and V (null: every unit uses f32 MFMAs):
+    // [tile - t0][kv head][K block | V block], each block 16 keys x D dims
+    // x (hi, lo) f16 in the MFMA operand order (prefill_split_kernel), and
+    // one flag per (tile, kv head), set when the tile's rows hold a value
+    // the split does not carry.
+    const _Float16 *planes;
+    uint32_t plane_bytes;
+    int64_t t0;
+    const int *tile_flags;
 };
+
+// Conversion of the rows a prefill call attends, keys [row_lo, row_hi), into
+// the split-f16 planes, one 16-key tile per (tile, kv head); rows of a tile
+// outside the range are zeros.
+struct SplitK {
+    const float *k;
+    const float *v;
+    int64_t row_stride;
+    int64_t kv_origin;
+    int64_t row_lo, row_hi;
+    int64_t t0;
+    int n_tiles;
+    _Float16 *planes;
+    int *tile_flags;
+};
+
+// K block of a tile: for each 32-dim chunk u and part (hi, lo), 64 lanes x 8
+// halves, lane 16g + c holding key c, dims 32u + 8g .. +7 -- the A operand of
+// the score MFMA (S^T = K Q^T).  V block: for each O^T tile T (dims
+// 64(T/4) + 4i + T%4, i < 16, the f32 path's accumulator order), 64 lanes x
+// 8 halves, lane 16g + c holding dim 64(T/4) + 4c + T%4 of keys 4g .. 4g+3,
+// hi parts then lo parts -- the A operand of O^T += V^T P^T, whose B operand
+// is the lane's own four weights (keys 4g .. 4g+3, the score MFMA's output
+// layout) twice.  Every block is one contiguous run of 16-byte lane slots,
+// which the prefill kernel copies to LDS unchanged.
+template <int D>
+__global__ __launch_bounds__(256) void prefill_split_kernel(SplitK s) {
+    constexpr int VS = D + 4;  // staged V row, padded against bank conflicts
+    __shared__ float vt[16 * VS];
+    const int tid = threadIdx.x, kvh = blockIdx.y, n_kv = gridDim.y;
+    for (int tt = blockIdx.x; tt < s.n_tiles; tt += gridDim.x) {
+        const int64_t key0 = 16 * (s.t0 + tt);
+        _Float16 *kb = s.planes + ((int64_t)tt * n_kv + kvh) * (64 * D);
+        _Float16 *vb = kb + 32 * D;
+        bool bad = false;
+        for (int it = tid; it < 2 * D; it += 256) {  // (D/32 chunks) x 64 lanes
+            const int uu = it >> 6, lane = it & 63, g = lane >> 4, c = lane & 15;
+            const int64_t pos = key0 + c;
+            f32x4 a = {0.0f, 0.0f, 0.0f, 0.0f}, b = a;
+            if (pos >= s.row_lo && pos < s.row_hi) {
+                const float *src = s.k + (pos - s.kv_origin) * s.row_stride + (int64_t)kvh * D + 32 * uu + 8 * g;
+                a = *(const f32x4 *)src;
+                b = *(const f32x4 *)(src + 4);
+            }
+            f16x8 hi, lo;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                _Float16 h, l;
+                split_f16<true>(a[j], h, l, bad);
+                hi[j] = h;
+                lo[j] = l;
+                split_f16<true>(b[j], h, l, bad);
+                hi[4 + j] = h;
+                lo[4 + j] = l;
+            }
+            *(f16x8 *)(kb + ((uu * 2 + 0) * 64 + lane) * 8) = hi;
+            *(f16x8 *)(kb + ((uu * 2 + 1) * 64 + lane) * 8) = lo;
+        }
+        __syncthreads();  // the previous tile's staged V rows are consumed
+        for (int f = tid; f < 4 * D; f += 256) {  // 16 rows x D/4 vectors
+            const int key = f / (D / 4), c4 = f % (D / 4);
+            const int64_t pos = key0 + key;
+            f32x4 x = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (pos >= s.row_lo && pos < s.row_hi)
+                x = *(const f32x4 *)(s.v + (pos - s.kv_origin) * s.row_stride + (int64_t)kvh * D + 4 * c4);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) vt[key * VS + 4 * c4 + i] = x[i];
+        }
+        __syncthreads();
+        for (int it = tid; it < 4 * D; it += 256) {  // (D/16 tiles) x 64 lanes
+            const int T = it >> 6, lane = it & 63, g = lane >> 4, c = lane & 15;
+            const int dim = 64 * (T >> 2) + 4 * c + (T & 3);
+            f16x8 hl;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                _Float16 h, l;
+                split_f16<false>(vt[(4 * g + r) * VS + dim], h, l, bad);
+                hl[r] = h;
+                hl[4 + r] = l;
+            }
+            *(f16x8 *)(vb + (T * 64 + lane) * 8) = hl;
+        }
+        // Zero rows (outside the range) never raise the flag.
+        bad = __syncthreads_or(bad);
+        if (tid == 0) s.tile_flags[(int64_t)tt * n_kv + kvh] = bad ? 1 : 0;
+    }
+}
 
 __device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -156,8 +298,21 @@ struct PrefillShape {
 
 // One unit: the rows of position block u.block against its key tiles
 // [u.t_lo, u.t_hi), leaving the block's output or the unit's partial.
-template <int D>
-__device__ __forceinline__ void prefill_unit(const PrefillK &p, const PrefillUnit u) {
+// SPLIT16: products as split-f16 MFMAs from the planes; such a unit first
+// checks that its q rows and tiles are carried exactly by the split, and
+// returns false (having written nothing) when they are not, for the caller
+// to run the f32 form.  The f32 form reads K/V rows directly and returns
+// true.
+// The kernel's LDS arrays (declared there, so that both forms of the unit
+// share them).
+struct PrefillLds {
+    f32x4 *k0, *v0, *k1, *v1;
+    f32x4 (*s0)[64], (*s1)[64];
+    int *nf_tile;
+};
+
+template <int D, bool SPLIT16>
+__device__ __forceinline__ bool prefill_unit(const PrefillK &p, const PrefillUnit u, const PrefillLds &L) {
     using S = PrefillShape<D>;
     constexpr int DH = S::DH;
     constexpr int NU = DH / 32;  // 32-dim K chunks per wave
@@ -186,16 +341,10 @@ __device__ __forceinline__ void prefill_unit(const PrefillK &p, const PrefillUni
     const int64_t win = p.window;
     const int d0 = half * DH;  // first dim of this wave
 
-    // Double-buffered K and V tiles (TPS per buffer, tile j at j*TILE_F4) and
-    // partial S^T of the D halves, each buffer its own array: the tiles being
-    // loaded and the tiles being read are then distinct objects, so the
-    // compiler need not wait for the former's loads before reading the
-    // latter.  The epilogue reuses the four tile arrays.
-    __shared__ f32x4 lds_k0[TPS * TILE_F4], lds_v0[TPS * TILE_F4], lds_k1[TPS * TILE_F4], lds_v1[TPS * TILE_F4];
-    __shared__ f32x4 lds_s0[S::WAVES][64], lds_s1[S::WAVES][64];
-    // Per wave group: 1 + the index of the last edge tile whose V held a
-    // non-finite value (see step()).
-    __shared__ int nf_tile[S::KSPLIT];
+    f32x4 *const lds_k0 = L.k0, *const lds_v0 = L.v0, *const lds_k1 = L.k1, *const lds_v1 = L.v1;
+    f32x4(*const lds_s0)[64] = L.s0;
+    f32x4(*const lds_s1)[64] = L.s1;
+    int *const nf_tile = L.nf_tile;
 
     // K/V tiles go straight from memory to LDS (buffer_load ... lds: lane l
     // of a wavefront writes the 16 bytes it loads to LDS base + 16*l), so the
@@ -217,28 +366,51 @@ __device__ __forceinline__ void prefill_unit(const PrefillK &p, const PrefillUni
         __builtin_amdgcn_make_buffer_rsrc((void *)(p.k + first), 0, (n_rows - 1) * stride * 4 + D * 4, kBufferWord3);
     const __amdgpu_buffer_rsrc_t vrs =
         __builtin_amdgcn_make_buffer_rsrc((void *)(p.v + first), 0, (n_rows - 1) * stride * 4 + D * 4, kBufferWord3);
+    // Split form: one resource over all planes; a tile's K block of this KV
+    // head is 64*D contiguous bytes (its V block follows), copied slot for
+    // slot.
+    const __amdgpu_buffer_rsrc_t prs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)p.planes, 0, (int)p.plane_bytes, kBufferWord3);
     uint32_t koffs[PER_THREAD], voffs[PER_THREAD];
 #pragma unroll
     for (int e = 0; e < PER_THREAD; ++e) {
         const int f = (e * S::WAVES + wave) * 64 + lane;
-        const int key = f & 15, rest = f >> 4;
-        const int dim = 32 * (rest >> 3) + 8 * ((rest >> 1) & 3) + 4 * (rest & 1);
-        koffs[e] = (uint32_t)(key * stride + dim) * 4u;
-        voffs[e] = (uint32_t)((f / (D / 4)) * stride + 4 * (f % (D / 4))) * 4u;
+        if constexpr (SPLIT16) {
+            koffs[e] = 16u * (uint32_t)f;
+            voffs[e] = 16u * (uint32_t)f + 64u * D;
+        } else {
+            const int key = f & 15, rest = f >> 4;
+            const int dim = 32 * (rest >> 3) + 8 * ((rest >> 1) & 3) + 4 * (rest & 1);
+            koffs[e] = (uint32_t)(key * stride + dim) * 4u;
+            voffs[e] = (uint32_t)((f / (D / 4)) * stride + 4 * (f % (D / 4))) * 4u;
+        }
     }
     // Load i (of 2*PER_THREAD) of tile t: K slots for even i, V for odd.
     auto issue_part = [&](int t, int i, f32x4 *kb, f32x4 *vb) {
-        const uint32_t toff = (uint32_t)((16LL * t - block_lo) * stride * 4);  // wraps below block_lo: out of range
         const int e = i >> 1, slot = (e * S::WAVES + wave) * 64;
-        if (i & 1)
-            load_to_lds(vrs, vb + slot, voffs[e] + toff);
-        else
-            load_to_lds(krs, kb + slot, koffs[e] + toff);
+        if constexpr (SPLIT16) {
+            const uint32_t toff = (uint32_t)(((t - p.t0) * (int64_t)gridDim.y + kvh) * (128LL * D));
+            load_to_lds(prs, (i & 1) ? vb + slot : kb + slot, ((i & 1) ? voffs[e] : koffs[e]) + toff);
+        } else {
+            const uint32_t toff = (uint32_t)((16LL * t - block_lo) * stride * 4);  // wraps below block_lo: out of range
+            if (i & 1)
+                load_to_lds(vrs, vb + slot, voffs[e] + toff);
+            else
+                load_to_lds(krs, kb + slot, koffs[e] + toff);
+        }
     };
     auto issue_tile = [&](int t, f32x4 *kb, f32x4 *vb) {
 #pragma unroll
         for (int i = 0; i < 2 * PER_THREAD; ++i) issue_part(t, i, kb, vb);
     };
+
+    // The split form issues its first tiles before it knows whether it will
+    // use them, so that their latency overlaps the q loads and the check.
+    if constexpr (SPLIT16) {
+#pragma unroll
+        for (int j = 0; j < TPS; ++j)
+            issue_tile(u.t_lo + j < u.t_hi ? u.t_lo + j : u.t_hi - 1, lds_k0 + j * TILE_F4, lds_v0 + j * TILE_F4);
+    }
 
     // Q^T (B operand): lane (g, c) holds q[row c][d0 + 32u + 8g + j].
     float qreg[NU][8];
@@ -254,6 +426,29 @@ __device__ __forceinline__ void prefill_unit(const PrefillK &p, const PrefillUni
                 qreg[uu][j] = a[j];
                 qreg[uu][4 + j] = b[j];
             }
+        }
+    }
+    // Split form: Q^T as hi and lo halves, in the same lanes.  The unit runs
+    // in f32 instead when a q value or a tile flag says the split does not
+    // carry its inputs exactly (the tiles issued above land first: the LDS
+    // they write is the f32 form's too).
+    f16x8 qh[SPLIT16 ? NU : 1], ql[SPLIT16 ? NU : 1];
+    if constexpr (SPLIT16) {
+        bool off = false;
+#pragma unroll
+        for (int uu = 0; uu < NU; ++uu)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                _Float16 h, lo;
+                split_f16<true>(qreg[uu][j], h, lo, off);
+                qh[uu][j] = h;
+                ql[uu][j] = lo;
+            }
+        for (int tt = u.t_lo + tid; tt < u.t_hi; tt += S::THREADS)
+            off |= p.tile_flags[(int64_t)(tt - p.t0) * gridDim.y + kvh] != 0;
+        if (__syncthreads_or(off)) {
+            __builtin_amdgcn_s_waitcnt(kVmcntZero);
+            return false;
         }
     }
 
@@ -304,7 +499,45 @@ __device__ __forceinline__ void prefill_unit(const PrefillK &p, const PrefillUni
         // with an odd tile count) only issues its share of the next loads:
         // its scores are all masked below.
         f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (live) {
+        if (SPLIT16 && live) {
+            // Split form: per 32-dim chunk the K hi and lo operands (one
+            // 16-byte lane slot each) and three MFMAs on three accumulators
+            // (hi.hi, hi.lo, lo.hi), so consecutive MFMAs never wait on each
+            // other.
+            f32x4 acc2 = {0.0f, 0.0f, 0.0f, 0.0f};
+            f32x4 kc[2][2];
+            auto read_k = [&](int uu, f32x4(&dst)[2]) {
+                const int ug = d0 / 32 + uu;
+                dst[0] = kt[(ug * 2 + 0) * 64 + lane];
+                dst[1] = kt[(ug * 2 + 1) * 64 + lane];
+            };
+            read_k(0, kc[0]);
+#pragma unroll
+            for (int uu = 0; uu < NU; ++uu) {
+                if (uu + 1 < NU) read_k(uu + 1, kc[(uu + 1) & 1]);
+                static_assert(NL % NU == 0 || NU % NL == 0, "loads spread over the chunks");
+                if constexpr (NL >= NU) {
+#pragma unroll
+                    for (int i = uu * (NL / NU); i < (uu + 1) * (NL / NU); ++i) load(i);
+                } else if (uu % (NU / NL) == 0) {
+                    load(uu / (NU / NL));
+                }
+                const f16x8 kh = __builtin_bit_cast(f16x8, kc[uu & 1][0]);
+                const f16x8 kl = __builtin_bit_cast(f16x8, kc[uu & 1][1]);
+                acc0 = split_mfma(kh, qh[uu], acc0);
+                acc1 = split_mfma(kh, ql[uu], acc1);
+                acc2 = split_mfma(kl, qh[uu], acc2);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
+#pragma unroll
+            for (int uu = 0; uu < NU; ++uu) {
+                if (uu + 1 < NU) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);       // DS read
+                __builtin_amdgcn_sched_group_barrier(0x010, NL >= NU ? NL / NU : 1, 0);  // VMEM
+                __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);                        // MFMA
+            }
+            acc0 += (acc1 + acc2) * kLoUnscale;
+            acc1 = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        } else if (!SPLIT16 && live) {
             f32x4 kc[2][2];
             auto read_k = [&](int uu, f32x4(&dst)[2]) {
                 const int ug = d0 / 32 + uu;
@@ -382,7 +615,7 @@ __device__ __forceinline__ void prefill_unit(const PrefillK &p, const PrefillUni
         // Lazy rescaling: a row keeps its reference max m until a score
         // exceeds it by more than kRescaleSlack (p < 2^32 meanwhile, safe in
         // f32), so O is rescaled about once per row rather than every tile.
-        if (__any(mt > m + kRescaleSlack)) {
+        if (__any(mt > m + (SPLIT16 ? kRescaleSlackSplit : kRescaleSlack))) {
             const float m_new = fmaxf(m, mt);
             const float alpha = (m_new == -INFINITY) ? 1.0f : exp2_fast((m - m_new) * kLog2e);
             l *= alpha;
@@ -392,7 +625,10 @@ __device__ __forceinline__ void prefill_unit(const PrefillK &p, const PrefillUni
         }
         float pr[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) pr[r] = (m == -INFINITY) ? 0.0f : exp2_fast((sv[r] - m) * kLog2e);
+        for (int r = 0; r < 4; ++r)
+            pr[r] = (m == -INFINITY) ? 0.0f
+                                     : (SPLIT16 ? exp2_fast((sv[r] - m) * kLog2e + (float)kPScale)
+                                                : exp2_fast((sv[r] - m) * kLog2e));
         l += (pr[0] + pr[1]) + (pr[2] + pr[3]);
 
         // Edge tiles: some row of the block masks keys of the tile that
@@ -403,9 +639,10 @@ __device__ __forceinline__ void prefill_unit(const PrefillK &p, const PrefillUni
         // non-finite values replaced by 0 in LDS before the product, and if
         // it held any, their p * v terms are added afterwards, from memory, to
         // the rows that attend them.  (Rows outside [block_lo, last_pos]
-        // already read as 0.)  Steps with no edge tile skip all of this.
+        // already read as 0.)  Steps with no edge tile skip all of this, and
+        // so does the split form, whose tiles hold finite values only.
         bool fix = false;
-        if (!exact(t) || (TPS == 2 && !exact(t + 1))) {  // uniform in the workgroup
+        if (!SPLIT16 && (!exact(t) || (TPS == 2 && !exact(t + 1)))) {  // uniform in the workgroup
             if (!(live && whole)) {
                 constexpr int GL = 64 * S::RWAVES;  // lanes of the waves sharing this V tile
                 f32x4 *vs = vb + kpar * TILE_F4;
@@ -433,9 +670,52 @@ __device__ __forceinline__ void prefill_unit(const PrefillK &p, const PrefillUni
             fix = !(live && whole) && nf_tile[kpar] == tw + 1;
         }
 
+        // Split form: O^T += V^T . P^T with the 32 k-slots of an MFMA as
+        // (keys 4g .. 4g+3 of lane group g) x (V hi, V lo): the B operand is
+        // the lane's four weights twice, as hi halves, then as lo halves in a
+        // second MFMA on the same V operand (V.p = Vhi.phi + Vlo.phi + Vhi.plo
+        // + Vlo.plo).  Two O^T tiles at a time, so that no MFMA waits on the
+        // one before it; their V operands are read one pair ahead.
+        if (SPLIT16 && live) {
+            f16x8 ph, pl;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const _Float16 h = (_Float16)pr[r];
+                const _Float16 lo = (_Float16)(pr[r] - (float)h);
+                ph[r] = h;
+                ph[4 + r] = h;
+                pl[r] = lo;
+                pl[4 + r] = lo;
+            }
+            static_assert(NT % 2 == 0, "O^T tiles in pairs");
+            const f32x4 *vt = vb + kpar * TILE_F4 + (d0 / 16) * 64 + lane;
+            f32x4 vc[2][2];
+            vc[0][0] = vt[0];
+            vc[0][1] = vt[64];
+#pragma unroll
+            for (int T = 0; T < NT; T += 2) {
+                const int sl = (T / 2) & 1;
+                if (T + 2 < NT) {
+                    vc[sl ^ 1][0] = vt[(T + 2) * 64];
+                    vc[sl ^ 1][1] = vt[(T + 3) * 64];
+                }
+                const f16x8 a0 = __builtin_bit_cast(f16x8, vc[sl][0]);
+                const f16x8 a1 = __builtin_bit_cast(f16x8, vc[sl][1]);
+                o[T] = split_mfma(a0, ph, o[T]);
+                o[T + 1] = split_mfma(a1, ph, o[T + 1]);
+                o[T] = split_mfma(a0, pl, o[T]);
+                o[T + 1] = split_mfma(a1, pl, o[T + 1]);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
+#pragma unroll
+            for (int T = 0; T < NT; T += 2) {
+                if (T + 2 < NT) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
+                __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);                   // MFMA
+            }
+        }
         // O^T += V^T . P^T over the tile's 16 keys (k-step r: keys 4g + r),
         // operand (r, U) read from LDS one step ahead as the K operands are.
-        if (live) {
+        if (!SPLIT16 && live) {
             constexpr int NPV = 4 * NV;
             f32x4 vc[2];
             auto read_v = [&](int idx, f32x4 &dst) {
@@ -489,9 +769,11 @@ __device__ __forceinline__ void prefill_unit(const PrefillK &p, const PrefillUni
             }
         }
     };
+    if constexpr (!SPLIT16) {
 #pragma unroll
-    for (int j = 0; j < TPS; ++j)
-        issue_tile(u.t_lo + j < u.t_hi ? u.t_lo + j : u.t_hi - 1, lds_k0 + j * TILE_F4, lds_v0 + j * TILE_F4);
+        for (int j = 0; j < TPS; ++j)
+            issue_tile(u.t_lo + j < u.t_hi ? u.t_lo + j : u.t_hi - 1, lds_k0 + j * TILE_F4, lds_v0 + j * TILE_F4);
+    }
     int t = u.t_lo;
     for (; t + TPS < u.t_hi; t += 2 * TPS) {
         step(t, lds_k0, lds_v0, lds_s0, lds_k1, lds_v1);
@@ -534,9 +816,11 @@ __device__ __forceinline__ void prefill_unit(const PrefillK &p, const PrefillUni
         if (result) {
 #pragma unroll
             for (int i = 0; i < NT; ++i) po[(wave * NT + i) * 64 + lane] = o[i];
-            if (g == 0 && half == 0) p.part_ml[sl * (kWaves * kRowsPerWave) + rg * kRowsPerWave + c] = float2{m, lt};
+            // The split form's weights carry 2^kPScale: fold it into m.
+            const float mr = (SPLIT16 && m != -INFINITY) ? m - kPScaleNat : m;
+            if (g == 0 && half == 0) p.part_ml[sl * (kWaves * kRowsPerWave) + rg * kRowsPerWave + c] = float2{mr, lt};
         }
-        return;
+        return true;
     }
     // Single unit: normalise and write row-major through LDS (coalesced).
     __syncthreads();  // every wave is done with the tile buffers (no tile load is in flight)
@@ -556,7 +840,7 @@ __device__ __forceinline__ void prefill_unit(const PrefillK &p, const PrefillUni
                 for (int r = 0; r < 4; ++r) tr[c * DH + 64 * U + 4 * (4 * g + r) + i] = o[4 * U + i][r] * inv;
     }
     __syncthreads();
-    if (!result) return;
+    if (!result) return true;
 #pragma unroll
     for (int e = 0; e < kRowsPerWave * DH / 4 / 64; ++e) {
         const int f = lane + 64 * e;
@@ -566,17 +850,37 @@ __device__ __forceinline__ void prefill_unit(const PrefillK &p, const PrefillUni
         float *orow = p.out + ((rpos - p.pos0) * p.n_heads + kvh * kGroup + (row & 7)) * D + d0;
         *(f32x4 *)(orow + 4 * c4) = *(const f32x4 *)(tr + row * DH + 4 * c4);
     }
+    return true;
 }
 
-// A workgroup runs its units in turn (the host's schedule).
+// A workgroup runs its units in turn (the host's schedule), each in the
+// split-f16 form when the call has planes and the unit's inputs allow it,
+// else with f32 MFMAs.
 template <int D>
 __global__ __launch_bounds__(PrefillShape<D>::THREADS, 1) void prefill_kernel(PrefillK p) {
+    using S = PrefillShape<D>;
+    constexpr int TILE_F4 = 16 * D / 4;
+    // Double-buffered K and V tiles (TPS per buffer, tile j at j*TILE_F4) and
+    // partial S^T of the D halves, each buffer its own array: the tiles being
+    // loaded and the tiles being read are then distinct objects, so the
+    // compiler need not wait for the former's loads before reading the
+    // latter.  The epilogue reuses the four tile arrays.
+    __shared__ f32x4 lds_k0[S::TPS * TILE_F4], lds_v0[S::TPS * TILE_F4], lds_k1[S::TPS * TILE_F4],
+        lds_v1[S::TPS * TILE_F4];
+    __shared__ f32x4 lds_s0[S::WAVES][64], lds_s1[S::WAVES][64];
+    // Per wave group: 1 + the index of the last edge tile whose V held a
+    // non-finite value (see the unit's step()).
+    __shared__ int nf_tile[S::KSPLIT];
+    const PrefillLds L{lds_k0, lds_v0, lds_k1, lds_v1, lds_s0, lds_s1, nf_tile};
     const int first = p.bin_start[blockIdx.x], end = p.bin_start[blockIdx.x + 1];
     for (int i = first; i < end; ++i) {
         // The previous unit's waves are done with the tile buffers (its
         // spare tile loads landed before its epilogue).
         if (i > first) __syncthreads();
-        prefill_unit<D>(p, p.units[i]);
+        const PrefillUnit u = p.units[i];
+        if (p.planes != nullptr && prefill_unit<D, true>(p, u, L)) continue;
+        if (p.planes != nullptr) __syncthreads();  // the declined split form's tiles have landed
+        prefill_unit<D, false>(p, u, L);
     }
 }
 
@@ -1071,14 +1375,54 @@ int launch_prefill(g4_ctx *ctx, const PrefillArgs &a, hipStream_t stream) {
     p.n_slots = pl.n_slots;
     p.status = ctx->status_dev;
     const int D = a.head_dim;
-    if (pl.n_slots > 0) {
-        const size_t per_slot = (size_t)a.n_kv_heads * kWaves * kRowsPerWave;
-        const size_t obytes = (size_t)pl.n_slots * per_slot * D * sizeof(float);
-        const size_t bytes = obytes + (size_t)pl.n_slots * per_slot * sizeof(float2) + 256;
+    // Workspace: the partials of split blocks, then the split-f16 planes of
+    // the attended rows and their tile flags.
+    auto up = [](size_t x) { return (x + 255) / 256 * 256; };
+    const size_t per_slot = (size_t)a.n_kv_heads * kWaves * kRowsPerWave;
+    const size_t obytes = up((size_t)pl.n_slots * per_slot * D * sizeof(float));
+    const size_t mlbytes = up((size_t)pl.n_slots * per_slot * sizeof(float2));
+    const int64_t row_lo = (a.window > 0 && a.pos0 + 1 > a.window) ? a.pos0 + 1 - a.window : 0;
+    const int64_t row_hi = a.pos0 + a.N;
+    const int64_t t0 = row_lo / 16, n_tiles = (row_hi - 1) / 16 + 1 - t0;
+    const size_t plane_bytes = (size_t)n_tiles * a.n_kv_heads * 128 * D;
+    // The split form: f16 products carry any |x| < 2^15 to f32 accuracy; the
+    // planes are addressed with 32-bit offsets; a scale beyond 2^32 could
+    // take scores near the f32 limit, where only the f32 form's rounding is
+    // the reference's.
+    const bool split = !ctx->prefill_exact && plane_bytes < (1ull << 31) && std::isfinite(a.scale) &&
+                       std::fabs(a.scale) <= 4294967296.0f;
+    const size_t bytes = obytes + mlbytes + (split ? up(plane_bytes) + up((size_t)n_tiles * a.n_kv_heads * 4) : 0);
+    if (bytes > 0) {
         rc = ensure_workspace(ctx, bytes, stream);
         if (rc != G4_OK) return rc;
-        p.part_o = (float *)ctx->ws.ptr;
-        p.part_ml = (float2 *)((char *)ctx->ws.ptr + (obytes + 255) / 256 * 256);
+        char *w = (char *)ctx->ws.ptr;
+        p.part_o = (float *)w;
+        p.part_ml = (float2 *)(w + obytes);
+        if (split) {
+            p.planes = (const _Float16 *)(w + obytes + mlbytes);
+            p.plane_bytes = (uint32_t)plane_bytes;
+            p.t0 = t0;
+            p.tile_flags = (const int *)(w + obytes + mlbytes + up(plane_bytes));
+        }
+    }
+    if (split) {
+        SplitK s{};
+        s.k = a.k;
+        s.v = a.v;
+        s.row_stride = a.row_stride;
+        s.kv_origin = a.kv_origin;
+        s.row_lo = row_lo;
+        s.row_hi = row_hi;
+        s.t0 = t0;
+        s.n_tiles = (int)n_tiles;
+        s.planes = (_Float16 *)p.planes;
+        s.tile_flags = (int *)p.tile_flags;
+        const dim3 sg((unsigned)std::min<int64_t>(n_tiles, 1024), (unsigned)a.n_kv_heads);
+        if (D == 256)
+            hipLaunchKernelGGL(prefill_split_kernel<256>, sg, dim3(256), 0, stream, s);
+        else
+            hipLaunchKernelGGL(prefill_split_kernel<512>, sg, dim3(256), 0, stream, s);
+        G4_HIP(hipGetLastError());
     }
     dim3 grid((unsigned)pl.n_bins, (unsigned)a.n_kv_heads);
     if (D == 256)

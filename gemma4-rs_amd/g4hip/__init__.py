@@ -56,6 +56,7 @@ _SIGS = {
     "g4_release": (c_int, [c_vp]),
     "g4_check_status": (c_int, [c_vp, c_vp]),
     "g4_set_decode_chunk": (c_int, [c_vp, c_i64]),
+    "g4_set_prefill_exact": (c_int, [c_vp, c_int]),
     "g4_alloc": (c_int, [c_vp, c_size, ctypes.POINTER(c_vp)]),
     "g4_free": (c_int, [c_vp, c_vp]),
     "g4_copy_to_device": (c_int, [c_vp, c_vp, c_vp, c_size]),
@@ -245,6 +246,10 @@ class Context:
 
     def set_decode_chunk(self, keys):
         _raise(lib().g4_set_decode_chunk(self.handle, keys))
+
+    def set_prefill_exact(self, exact):
+        """1: prefill with f32 MFMA products only; 0: split-f16 products where the inputs allow."""
+        _raise(lib().g4_set_prefill_exact(self.handle, int(exact)))
 
     # -- device memory (caller-owned buffers without torch) ----------------
     def alloc(self, nbytes):

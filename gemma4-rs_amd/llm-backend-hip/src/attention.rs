@@ -227,6 +227,13 @@ impl HipPort {
         // SAFETY: ctx is live.
         self.context().call(|ctx| unsafe { ffi::g4_set_decode_chunk(ctx, keys) })
     }
+
+    /// Prefill products: `true` = f32 MFMAs only; `false` (default) = split-f16
+    /// MFMAs for every work unit whose inputs are finite and below 2^15.
+    pub fn set_prefill_exact(&self, exact: bool) -> Result<(), EngError> {
+        // SAFETY: ctx is live.
+        self.context().call(|ctx| unsafe { ffi::g4_set_prefill_exact(ctx, exact as c_int) })
+    }
 }
 
 /// `layer_attention_kind` (idea/mod.rs:148-156): true on global layers.

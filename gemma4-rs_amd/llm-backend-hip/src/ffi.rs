@@ -52,6 +52,7 @@ extern "C" {
     pub fn g4_release(ctx: *mut G4Ctx) -> c_int;
     pub fn g4_check_status(ctx: *mut G4Ctx, stream: *mut c_void) -> c_int;
     pub fn g4_set_decode_chunk(ctx: *mut G4Ctx, keys: i64) -> c_int;
+    pub fn g4_set_prefill_exact(ctx: *mut G4Ctx, exact: c_int) -> c_int;
     pub fn g4_alloc(ctx: *mut G4Ctx, bytes: usize, ptr_dev: *mut *mut c_void) -> c_int;
     pub fn g4_free(ctx: *mut G4Ctx, ptr_dev: *mut c_void) -> c_int;
     pub fn g4_copy_to_device(

@@ -64,6 +64,13 @@ int g4_release(g4_ctx *ctx);
 int g4_check_status(g4_ctx *ctx, g4_stream stream);
 /* Tuning: keys per split-K work item of the decode kernels (0 = automatic). */
 int g4_set_decode_chunk(g4_ctx *ctx, int64_t keys);
+/* Tuning: 1 = prefill computes every product with f32 MFMAs; 0 (default) =
+ * split-f16 MFMA products (each f32 operand as an f16 hi + lo pair, three
+ * f16 products per f32 product, f32 accumulation) for every work unit whose
+ * q rows and K/V rows are finite and below 2^15 in magnitude, f32 MFMAs for
+ * the others.  Both match the f32 reference within its tolerance; the
+ * engine has no counterpart (a backend precision knob). */
+int g4_set_prefill_exact(g4_ctx *ctx, int exact);
 
 /* ---------------------------------------------------------- device memory */
 /* Caller-owned device buffers on the context's device, so that a binding
