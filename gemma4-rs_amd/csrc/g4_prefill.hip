@@ -16,6 +16,12 @@
 // Computing S^T leaves lane (g, c) holding keys 4g..4g+3 of row c, which is
 // the B-operand layout P^T needs, so P stays in registers.
 //
+// Two forms of the same tiling, chosen per work unit: split-f16 products
+// (each f32 operand as an f16 hi + lo pair, v_mfma_f32_16x16x32_f16, K/V
+// read from planes a prepass writes in operand order; see split_f16) for
+// units whose inputs the split carries, and the f32 MFMA form above for the
+// others.  Both leave the same partial layout, so one merge serves both.
+//
 // Work balance: the causal triangle gives the last position blocks many more
 // tiles than the first, so a block's key range may be cut into units (at
 // most kPrefillMaxUnitsDev per block), and the host assigns every unit to a
@@ -137,8 +143,8 @@ struct PrefillK {
     // Split-f16 planes of K and V (null: every unit uses f32 MFMAs):
     // [tile - t0][kv head][K block | V block], each block 16 keys x D dims
     // x (hi, lo) f16 in the MFMA operand order (prefill_split_kernel), and
-    // one flag per (tile, kv head), set when the tile's rows hold a value
-    // the split does not carry.
+    // two flags per (tile, kv head), K's and V's, set when the block's rows
+    // hold a value the split does not carry.
     const _Float16 *planes;
     uint32_t plane_bytes;
     int64_t t0;
@@ -147,7 +153,7 @@ struct PrefillK {
 
 // Conversion of the rows a prefill call attends, keys [row_lo, row_hi), into
 // the split-f16 planes, one 16-key tile per (tile, kv head); rows of a tile
-// outside the range are zeros.
+// outside the range are zeros.  Flags: [tile][kv head][K, V].
 struct SplitK {
     const float *k;
     const float *v;
@@ -169,67 +175,82 @@ struct SplitK {
 // is the lane's own four weights (keys 4g .. 4g+3, the score MFMA's output
 // layout) twice.  Every block is one contiguous run of 16-byte lane slots,
 // which the prefill kernel copies to LDS unchanged.
+//
+// Workgroup (tile, kv head, z): z = 0 writes the K block, z = 1 the V block,
+// and its own flag.  A K thread makes the two slots (hi, lo) of one lane and
+// chunk from two 16-byte loads; a V thread makes the four slots T = 4U .. 4U+3
+// of one lane from four 16-byte loads (keys 4g .. 4g+3, dims 64U + 4c ..
+// +3), so every load is issued before any conversion waits.
 template <int D>
 __global__ __launch_bounds__(256) void prefill_split_kernel(SplitK s) {
-    constexpr int VS = D + 4;  // staged V row, padded against bank conflicts
-    __shared__ float vt[16 * VS];
-    const int tid = threadIdx.x, kvh = blockIdx.y, n_kv = gridDim.y;
-    for (int tt = blockIdx.x; tt < s.n_tiles; tt += gridDim.x) {
-        const int64_t key0 = 16 * (s.t0 + tt);
-        _Float16 *kb = s.planes + ((int64_t)tt * n_kv + kvh) * (64 * D);
-        _Float16 *vb = kb + 32 * D;
-        bool bad = false;
-        for (int it = tid; it < 2 * D; it += 256) {  // (D/32 chunks) x 64 lanes
-            const int uu = it >> 6, lane = it & 63, g = lane >> 4, c = lane & 15;
-            const int64_t pos = key0 + c;
-            f32x4 a = {0.0f, 0.0f, 0.0f, 0.0f}, b = a;
-            if (pos >= s.row_lo && pos < s.row_hi) {
-                const float *src = s.k + (pos - s.kv_origin) * s.row_stride + (int64_t)kvh * D + 32 * uu + 8 * g;
-                a = *(const f32x4 *)src;
-                b = *(const f32x4 *)(src + 4);
-            }
+    constexpr int KIT = 2 * D / 256;  // K lane slots per thread: (D/32 chunks) x 64 lanes
+    constexpr int VIT = D / 256;      // V lane groups per thread: (D/64) x 64 lanes
+    static_assert(KIT >= 1 && VIT >= 1, "head width of at least 256");
+    const int tid = threadIdx.x, kvh = blockIdx.y, n_kv = gridDim.y, tt = blockIdx.x;
+    const int64_t key0 = 16 * (s.t0 + tt);
+    _Float16 *kb = s.planes + ((int64_t)tt * n_kv + kvh) * (64 * D);
+    _Float16 *vb = kb + 32 * D;
+    auto row = [&](const float *base, int key) -> const float * {
+        const int64_t pos = key0 + key;
+        if (pos < s.row_lo || pos >= s.row_hi) return nullptr;
+        return base + (pos - s.kv_origin) * s.row_stride + (int64_t)kvh * D;
+    };
+    const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    bool bad = false;
+    if (blockIdx.z == 0) {
+        f32x4 x[KIT][2];
+#pragma unroll
+        for (int e = 0; e < KIT; ++e) {
+            const int it = tid + 256 * e, uu = it >> 6, g = (it >> 4) & 3, c = it & 15;
+            const float *r = row(s.k, c);
+            x[e][0] = r ? *(const f32x4 *)(r + 32 * uu + 8 * g) : zero;
+            x[e][1] = r ? *(const f32x4 *)(r + 32 * uu + 8 * g + 4) : zero;
+        }
+#pragma unroll
+        for (int e = 0; e < KIT; ++e) {
+            const int it = tid + 256 * e, uu = it >> 6, lane = it & 63;
             f16x8 hi, lo;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+            for (int j = 0; j < 8; ++j) {
                 _Float16 h, l;
-                split_f16<true>(a[j], h, l, bad);
+                split_f16<true>(x[e][j >> 2][j & 3], h, l, bad);
                 hi[j] = h;
                 lo[j] = l;
-                split_f16<true>(b[j], h, l, bad);
-                hi[4 + j] = h;
-                lo[4 + j] = l;
             }
             *(f16x8 *)(kb + ((uu * 2 + 0) * 64 + lane) * 8) = hi;
             *(f16x8 *)(kb + ((uu * 2 + 1) * 64 + lane) * 8) = lo;
         }
-        __syncthreads();  // the previous tile's staged V rows are consumed
-        for (int f = tid; f < 4 * D; f += 256) {  // 16 rows x D/4 vectors
-            const int key = f / (D / 4), c4 = f % (D / 4);
-            const int64_t pos = key0 + key;
-            f32x4 x = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (pos >= s.row_lo && pos < s.row_hi)
-                x = *(const f32x4 *)(s.v + (pos - s.kv_origin) * s.row_stride + (int64_t)kvh * D + 4 * c4);
+    } else {
+        f32x4 x[VIT][4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) vt[key * VS + 4 * c4 + i] = x[i];
-        }
-        __syncthreads();
-        for (int it = tid; it < 4 * D; it += 256) {  // (D/16 tiles) x 64 lanes
-            const int T = it >> 6, lane = it & 63, g = lane >> 4, c = lane & 15;
-            const int dim = 64 * (T >> 2) + 4 * c + (T & 3);
-            f16x8 hl;
+        for (int e = 0; e < VIT; ++e) {
+            const int it = tid + 256 * e, U = it >> 6, g = (it >> 4) & 3, c = it & 15;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                _Float16 h, l;
-                split_f16<false>(vt[(4 * g + r) * VS + dim], h, l, bad);
-                hl[r] = h;
-                hl[4 + r] = l;
+                const float *rp = row(s.v, 4 * g + r);
+                x[e][r] = rp ? *(const f32x4 *)(rp + 64 * U + 4 * c) : zero;
             }
-            *(f16x8 *)(vb + (T * 64 + lane) * 8) = hl;
         }
-        // Zero rows (outside the range) never raise the flag.
-        bad = __syncthreads_or(bad);
-        if (tid == 0) s.tile_flags[(int64_t)tt * n_kv + kvh] = bad ? 1 : 0;
+#pragma unroll
+        for (int e = 0; e < VIT; ++e) {
+            const int it = tid + 256 * e, U = it >> 6, lane = it & 63;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {  // T = 4U + i: dim 64U + 4c + i
+                f16x8 hl;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    _Float16 h, l;
+                    split_f16<false>(x[e][r][i], h, l, bad);
+                    hl[r] = h;
+                    hl[4 + r] = l;
+                }
+                *(f16x8 *)(vb + ((4 * U + i) * 64 + lane) * 8) = hl;
+            }
+        }
     }
+    // Zero rows (outside the range) never raise the flag.
+    bad = __syncthreads_or(bad);
+    if (tid == 0) s.tile_flags[((int64_t)tt * n_kv + kvh) * 2 + blockIdx.z] = bad ? 1 : 0;
 }
 
 __device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -444,8 +465,8 @@ __device__ __forceinline__ bool prefill_unit(const PrefillK &p, const PrefillUni
                 qh[uu][j] = h;
                 ql[uu][j] = lo;
             }
-        for (int tt = u.t_lo + tid; tt < u.t_hi; tt += S::THREADS)
-            off |= p.tile_flags[(int64_t)(tt - p.t0) * gridDim.y + kvh] != 0;
+        for (int f = 2 * u.t_lo + tid; f < 2 * u.t_hi; f += S::THREADS)  // (tile, K | V) flags
+            off |= p.tile_flags[((int64_t)(f / 2 - p.t0) * gridDim.y + kvh) * 2 + (f & 1)] != 0;
         if (__syncthreads_or(off)) {
             __builtin_amdgcn_s_waitcnt(kVmcntZero);
             return false;
@@ -499,45 +520,7 @@ __device__ __forceinline__ bool prefill_unit(const PrefillK &p, const PrefillUni
         // with an odd tile count) only issues its share of the next loads:
         // its scores are all masked below.
         f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (SPLIT16 && live) {
-            // Split form: per 32-dim chunk the K hi and lo operands (one
-            // 16-byte lane slot each) and three MFMAs on three accumulators
-            // (hi.hi, hi.lo, lo.hi), so consecutive MFMAs never wait on each
-            // other.
-            f32x4 acc2 = {0.0f, 0.0f, 0.0f, 0.0f};
-            f32x4 kc[2][2];
-            auto read_k = [&](int uu, f32x4(&dst)[2]) {
-                const int ug = d0 / 32 + uu;
-                dst[0] = kt[(ug * 2 + 0) * 64 + lane];
-                dst[1] = kt[(ug * 2 + 1) * 64 + lane];
-            };
-            read_k(0, kc[0]);
-#pragma unroll
-            for (int uu = 0; uu < NU; ++uu) {
-                if (uu + 1 < NU) read_k(uu + 1, kc[(uu + 1) & 1]);
-                static_assert(NL % NU == 0 || NU % NL == 0, "loads spread over the chunks");
-                if constexpr (NL >= NU) {
-#pragma unroll
-                    for (int i = uu * (NL / NU); i < (uu + 1) * (NL / NU); ++i) load(i);
-                } else if (uu % (NU / NL) == 0) {
-                    load(uu / (NU / NL));
-                }
-                const f16x8 kh = __builtin_bit_cast(f16x8, kc[uu & 1][0]);
-                const f16x8 kl = __builtin_bit_cast(f16x8, kc[uu & 1][1]);
-                acc0 = split_mfma(kh, qh[uu], acc0);
-                acc1 = split_mfma(kh, ql[uu], acc1);
-                acc2 = split_mfma(kl, qh[uu], acc2);
-            }
-            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
-#pragma unroll
-            for (int uu = 0; uu < NU; ++uu) {
-                if (uu + 1 < NU) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);       // DS read
-                __builtin_amdgcn_sched_group_barrier(0x010, NL >= NU ? NL / NU : 1, 0);  // VMEM
-                __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);                        // MFMA
-            }
-            acc0 += (acc1 + acc2) * kLoUnscale;
-            acc1 = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        } else if (!SPLIT16 && live) {
+        if (live) {
             f32x4 kc[2][2];
             auto read_k = [&](int uu, f32x4(&dst)[2]) {
                 const int ug = d0 / 32 + uu;
@@ -615,7 +598,7 @@ __device__ __forceinline__ bool prefill_unit(const PrefillK &p, const PrefillUni
         // Lazy rescaling: a row keeps its reference max m until a score
         // exceeds it by more than kRescaleSlack (p < 2^32 meanwhile, safe in
         // f32), so O is rescaled about once per row rather than every tile.
-        if (__any(mt > m + (SPLIT16 ? kRescaleSlackSplit : kRescaleSlack))) {
+        if (__any(mt > m + kRescaleSlack)) {
             const float m_new = fmaxf(m, mt);
             const float alpha = (m_new == -INFINITY) ? 1.0f : exp2_fast((m - m_new) * kLog2e);
             l *= alpha;
@@ -625,10 +608,7 @@ __device__ __forceinline__ bool prefill_unit(const PrefillK &p, const PrefillUni
         }
         float pr[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-            pr[r] = (m == -INFINITY) ? 0.0f
-                                     : (SPLIT16 ? exp2_fast((sv[r] - m) * kLog2e + (float)kPScale)
-                                                : exp2_fast((sv[r] - m) * kLog2e));
+        for (int r = 0; r < 4; ++r) pr[r] = (m == -INFINITY) ? 0.0f : exp2_fast((sv[r] - m) * kLog2e);
         l += (pr[0] + pr[1]) + (pr[2] + pr[3]);
 
         // Edge tiles: some row of the block masks keys of the tile that
@@ -639,10 +619,9 @@ __device__ __forceinline__ bool prefill_unit(const PrefillK &p, const PrefillUni
         // non-finite values replaced by 0 in LDS before the product, and if
         // it held any, their p * v terms are added afterwards, from memory, to
         // the rows that attend them.  (Rows outside [block_lo, last_pos]
-        // already read as 0.)  Steps with no edge tile skip all of this, and
-        // so does the split form, whose tiles hold finite values only.
+        // already read as 0.)  Steps with no edge tile skip all of this.
         bool fix = false;
-        if (!SPLIT16 && (!exact(t) || (TPS == 2 && !exact(t + 1)))) {  // uniform in the workgroup
+        if (!exact(t) || (TPS == 2 && !exact(t + 1))) {  // uniform in the workgroup
             if (!(live && whole)) {
                 constexpr int GL = 64 * S::RWAVES;  // lanes of the waves sharing this V tile
                 f32x4 *vs = vb + kpar * TILE_F4;
@@ -670,52 +649,9 @@ __device__ __forceinline__ bool prefill_unit(const PrefillK &p, const PrefillUni
             fix = !(live && whole) && nf_tile[kpar] == tw + 1;
         }
 
-        // Split form: O^T += V^T . P^T with the 32 k-slots of an MFMA as
-        // (keys 4g .. 4g+3 of lane group g) x (V hi, V lo): the B operand is
-        // the lane's four weights twice, as hi halves, then as lo halves in a
-        // second MFMA on the same V operand (V.p = Vhi.phi + Vlo.phi + Vhi.plo
-        // + Vlo.plo).  Two O^T tiles at a time, so that no MFMA waits on the
-        // one before it; their V operands are read one pair ahead.
-        if (SPLIT16 && live) {
-            f16x8 ph, pl;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const _Float16 h = (_Float16)pr[r];
-                const _Float16 lo = (_Float16)(pr[r] - (float)h);
-                ph[r] = h;
-                ph[4 + r] = h;
-                pl[r] = lo;
-                pl[4 + r] = lo;
-            }
-            static_assert(NT % 2 == 0, "O^T tiles in pairs");
-            const f32x4 *vt = vb + kpar * TILE_F4 + (d0 / 16) * 64 + lane;
-            f32x4 vc[2][2];
-            vc[0][0] = vt[0];
-            vc[0][1] = vt[64];
-#pragma unroll
-            for (int T = 0; T < NT; T += 2) {
-                const int sl = (T / 2) & 1;
-                if (T + 2 < NT) {
-                    vc[sl ^ 1][0] = vt[(T + 2) * 64];
-                    vc[sl ^ 1][1] = vt[(T + 3) * 64];
-                }
-                const f16x8 a0 = __builtin_bit_cast(f16x8, vc[sl][0]);
-                const f16x8 a1 = __builtin_bit_cast(f16x8, vc[sl][1]);
-                o[T] = split_mfma(a0, ph, o[T]);
-                o[T + 1] = split_mfma(a1, ph, o[T + 1]);
-                o[T] = split_mfma(a0, pl, o[T]);
-                o[T + 1] = split_mfma(a1, pl, o[T + 1]);
-            }
-            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
-#pragma unroll
-            for (int T = 0; T < NT; T += 2) {
-                if (T + 2 < NT) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
-                __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);                   // MFMA
-            }
-        }
         // O^T += V^T . P^T over the tile's 16 keys (k-step r: keys 4g + r),
         // operand (r, U) read from LDS one step ahead as the K operands are.
-        if (!SPLIT16 && live) {
+        if (live) {
             constexpr int NPV = 4 * NV;
             f32x4 vc[2];
             auto read_v = [&](int idx, f32x4 &dst) {
@@ -769,17 +705,194 @@ __device__ __forceinline__ bool prefill_unit(const PrefillK &p, const PrefillUni
             }
         }
     };
-    if constexpr (!SPLIT16) {
+    if constexpr (SPLIT16) {
+        // Software pipeline over steps s of TPS tiles: K(s) in k[s % 2], V(s)
+        // in v[s % 2], K loaded one step ahead of V.  Iteration s, after the
+        // step's one barrier: step s's full scores (the pair's partials,
+        // written at the end of iteration s-1), its mask, maximum and lazy
+        // rescale; then, in one straight-line block, the score MFMAs of step
+        // s+1 with the next loads and step s's weights (VALU) between them,
+        // and P.V(s); last, step s+1's partial scores go to the exchange slot
+        // that the next barrier publishes.  The two waves of a SIMD (the
+        // pair, at D = 512) thus no longer stop for a mid-step exchange, and
+        // the softmax runs beside the matrix pipe.
+        const int nsteps = (u.t_hi - u.t_lo + TPS - 1) / TPS;
+        auto tile_at = [&](int st, int j) {
+            const int tt = u.t_lo + TPS * st + j;
+            return tt < u.t_hi ? tt : u.t_hi - 1;  // past the end: the last tile again (unread)
+        };
+        // Partial S^T of step st's tile for this wave's group over its dims,
+        // from kt (that step's K buffer); load(i) for i < NL spread over the
+        // chunks.  A stale tile (past the unit) is computed anyway, from the
+        // finite values its buffer holds, and masked whole.
+        constexpr int NL = 2 * PER_THREAD * TPS;  // tile-part loads per step
+        static_assert(NL % NU == 0 || NU % NL == 0, "loads spread over the chunks");
+        auto part_scores = [&](const f32x4 *kb_, auto &&load) -> f32x4 {
+            const f32x4 *kt = kb_ + kpar * TILE_F4;
+            f32x4 a0 = {0.0f, 0.0f, 0.0f, 0.0f}, a1 = a0, a2 = a0;
+            f32x4 kc[2][2];
+            auto read_k = [&](int uu, f32x4(&dst)[2]) {
+                const int ug = d0 / 32 + uu;
+                dst[0] = kt[(ug * 2 + 0) * 64 + lane];
+                dst[1] = kt[(ug * 2 + 1) * 64 + lane];
+            };
+            read_k(0, kc[0]);
+#pragma unroll
+            for (int uu = 0; uu < NU; ++uu) {
+                if (uu + 1 < NU) read_k(uu + 1, kc[(uu + 1) & 1]);
+                if constexpr (NL >= NU) {
+#pragma unroll
+                    for (int i = uu * (NL / NU); i < (uu + 1) * (NL / NU); ++i) load(i);
+                } else if (uu % (NU / NL) == 0) {
+                    load(uu / (NU / NL));
+                }
+                const f16x8 kh = __builtin_bit_cast(f16x8, kc[uu & 1][0]);
+                const f16x8 kl = __builtin_bit_cast(f16x8, kc[uu & 1][1]);
+                a0 = split_mfma(kh, qh[uu], a0);
+                a1 = split_mfma(kh, ql[uu], a1);
+                a2 = split_mfma(kl, qh[uu], a2);
+            }
+            return a0 + (a1 + a2) * kLoUnscale;
+        };
+        // K(1); K(0) and V(0) were issued at the unit's start.
+#pragma unroll
+        for (int j = 0; j < TPS; ++j)
+#pragma unroll
+            for (int e = 0; e < PER_THREAD; ++e) issue_part(tile_at(1, j), 2 * e, lds_k1 + j * TILE_F4, nullptr);
+        __builtin_amdgcn_s_waitcnt(kVmcntZero);
+        __syncthreads();  // K(0), V(0), K(1) have landed
+        f32x4 sc_next;    // D = 256: the wave's own scores of the next step
+        {
+            const f32x4 part = part_scores(lds_k0, [](int) {});
+            if constexpr (S::SPLIT == 2)
+                lds_s0[wave][lane] = part;
+            else
+                sc_next = part;
+        }
+        // Iteration st: kn1 holds K(st+1), kfree receives K(st+2), vcur holds
+        // V(st), vnext receives V(st+1); xr holds step st's partials, xw
+        // receives step st+1's.
+        auto iter = [&](int st, const f32x4 *kn1, f32x4 *kfree, const f32x4 *vcur, f32x4 *vnext, f32x4(*xr)[64],
+                        f32x4(*xw)[64]) {
+            __builtin_amdgcn_s_waitcnt(kVmcntZero);
+            __syncthreads();  // K(st+1), V(st) and step st's partials are in; k(st), v(st-1) are free
+            f32x4 sc;
+            if constexpr (S::SPLIT == 2)
+                sc = xr[rg][lane] + xr[rg + kWaves][lane];  // half 0 + half 1, in that order
+            else
+                sc = sc_next;
+            const int tw = u.t_lo + TPS * st + kpar;
+            const bool live = S::KSPLIT == 1 || tw < u.t_hi;
+            float sv[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sv[r] = scaled ? sc[r] * p.scale : sc[r];
+            if (!live) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) sv[r] = -INFINITY;
+            } else if (!exact(tw)) {
+                const int64_t rel = pos - 16LL * tw;  // key - 16tw <= rel, and > rel - win
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int kr = 4 * g + r;
+                    if (!(kr <= rel && (win == 0 || kr > rel - win))) sv[r] = -INFINITY;
+                }
+            }
+            const float mx = __builtin_elementwise_maximum(__builtin_elementwise_maximum(sv[0], sv[1]),
+                                                           __builtin_elementwise_maximum(sv[2], sv[3]));
+            bad |= __builtin_amdgcn_classf(mx, 0x203);  // signalling/quiet NaN, +inf
+            const float mt = rows_max(mx);
+            if (__any(mt > m + kRescaleSlackSplit)) {
+                const float m_new = fmaxf(m, mt);
+                const float alpha = (m_new == -INFINITY) ? 1.0f : exp2_fast((m - m_new) * kLog2e);
+                l *= alpha;
+                m = m_new;
+#pragma unroll
+                for (int i = 0; i < NT; ++i) o[i] *= alpha;
+            }
+            // One straight-line block from here: the score MFMAs of step
+            // st+1 with this iteration's loads, step st's weights, P.V(st).
+            auto load = [&](int i) {
+                const int j = i / (2 * PER_THREAD), part = i % (2 * PER_THREAD);
+                if (part & 1)
+                    issue_part(tile_at(st + 1, j), part, nullptr, vnext + j * TILE_F4);
+                else
+                    issue_part(tile_at(st + 2, j), part, kfree + j * TILE_F4, nullptr);
+            };
+            const f32x4 part = part_scores(kn1, load);
+            float pr[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                pr[r] = (m == -INFINITY) ? 0.0f : exp2_fast((sv[r] - m) * kLog2e + (float)kPScale);
+            l += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+            f16x8 ph, pl;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const _Float16 h = (_Float16)pr[r];
+                const _Float16 lo = (_Float16)(pr[r] - (float)h);
+                ph[r] = h;
+                ph[4 + r] = h;
+                pl[r] = lo;
+                pl[4 + r] = lo;
+            }
+            // P.V(st); a stale tile's weights are 0 and its V is finite.
+            static_assert(NT % 2 == 0, "O^T tiles in pairs");
+            const f32x4 *vt = vcur + kpar * TILE_F4 + (d0 / 16) * 64 + lane;
+            f32x4 vc[2][2];
+            vc[0][0] = vt[0];
+            vc[0][1] = vt[64];
+#pragma unroll
+            for (int T = 0; T < NT; T += 2) {
+                const int sl = (T / 2) & 1;
+                if (T + 2 < NT) {
+                    vc[sl ^ 1][0] = vt[(T + 2) * 64];
+                    vc[sl ^ 1][1] = vt[(T + 3) * 64];
+                }
+                const f16x8 a0 = __builtin_bit_cast(f16x8, vc[sl][0]);
+                const f16x8 a1 = __builtin_bit_cast(f16x8, vc[sl][1]);
+                o[T] = split_mfma(a0, ph, o[T]);
+                o[T + 1] = split_mfma(a1, ph, o[T + 1]);
+                o[T] = split_mfma(a0, pl, o[T]);
+                o[T + 1] = split_mfma(a1, pl, o[T + 1]);
+            }
+            if constexpr (S::SPLIT == 2)
+                xw[wave][lane] = part;
+            else
+                sc_next = part;
+            // Order: K reads of chunk 0; per chunk the next chunk's K reads,
+            // its share of the loads, its three MFMAs and a few VALU of the
+            // weights; then P.V, two V reads per four MFMAs.
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
+#pragma unroll
+            for (int uu = 0; uu < NU; ++uu) {
+                if (uu + 1 < NU) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);       // DS read
+                __builtin_amdgcn_sched_group_barrier(0x010, NL >= NU ? NL / NU : 1, 0);  // VMEM
+                __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);                        // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);                        // VALU
+            }
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
+#pragma unroll
+            for (int T = 0; T < NT; T += 2) {
+                if (T + 2 < NT) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
+                __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);                   // MFMA
+            }
+        };
+        int st = 0;
+        for (; st + 1 < nsteps; st += 2) {
+            iter(st, lds_k1, lds_k0, lds_v0, lds_v1, lds_s0, lds_s1);
+            iter(st + 1, lds_k0, lds_k1, lds_v1, lds_v0, lds_s1, lds_s0);
+        }
+        if (st < nsteps) iter(st, lds_k1, lds_k0, lds_v0, lds_v1, lds_s0, lds_s1);
+    } else {
 #pragma unroll
         for (int j = 0; j < TPS; ++j)
             issue_tile(u.t_lo + j < u.t_hi ? u.t_lo + j : u.t_hi - 1, lds_k0 + j * TILE_F4, lds_v0 + j * TILE_F4);
+        int t = u.t_lo;
+        for (; t + TPS < u.t_hi; t += 2 * TPS) {
+            step(t, lds_k0, lds_v0, lds_s0, lds_k1, lds_v1);
+            step(t + TPS, lds_k1, lds_v1, lds_s1, lds_k0, lds_v0);
+        }
+        if (t < u.t_hi) step(t, lds_k0, lds_v0, lds_s0, lds_k1, lds_v1);
     }
-    int t = u.t_lo;
-    for (; t + TPS < u.t_hi; t += 2 * TPS) {
-        step(t, lds_k0, lds_v0, lds_s0, lds_k1, lds_v1);
-        step(t + TPS, lds_k1, lds_v1, lds_s1, lds_k0, lds_v0);
-    }
-    if (t < u.t_hi) step(t, lds_k0, lds_v0, lds_s0, lds_k1, lds_v1);
 
     if (__any(bad && row_valid) && lane == 0) atomicOr(p.status, kStatusNonFinite);
     __builtin_amdgcn_s_waitcnt(kVmcntZero);  // the last step's spare loads have landed
@@ -1391,7 +1504,7 @@ int launch_prefill(g4_ctx *ctx, const PrefillArgs &a, hipStream_t stream) {
     // the reference's.
     const bool split = !ctx->prefill_exact && plane_bytes < (1ull << 31) && std::isfinite(a.scale) &&
                        std::fabs(a.scale) <= 4294967296.0f;
-    const size_t bytes = obytes + mlbytes + (split ? up(plane_bytes) + up((size_t)n_tiles * a.n_kv_heads * 4) : 0);
+    const size_t bytes = obytes + mlbytes + (split ? up(plane_bytes) + up((size_t)n_tiles * a.n_kv_heads * 8) : 0);
     if (bytes > 0) {
         rc = ensure_workspace(ctx, bytes, stream);
         if (rc != G4_OK) return rc;
@@ -1417,7 +1530,7 @@ int launch_prefill(g4_ctx *ctx, const PrefillArgs &a, hipStream_t stream) {
         s.n_tiles = (int)n_tiles;
         s.planes = (_Float16 *)p.planes;
         s.tile_flags = (int *)p.tile_flags;
-        const dim3 sg((unsigned)std::min<int64_t>(n_tiles, 1024), (unsigned)a.n_kv_heads);
+        const dim3 sg((unsigned)n_tiles, (unsigned)a.n_kv_heads, 2);
         if (D == 256)
             hipLaunchKernelGGL(prefill_split_kernel<256>, sg, dim3(256), 0, stream, s);
         else
