@@ -40,6 +40,12 @@ for p in (ROOT, os.path.join(ROOT, "gemma4-rs_amd")):
 
 HBM_PEAK_GBS = 8000.0
 F32_MFMA_PEAK_TFLOPS = 157.3
+F16_MFMA_PEAK_TFLOPS = 2500.0
+# The prefill's split-f16 form executes 3 f16 MFMA products per score product
+# and 4 per weight x value product: 3.5 per counted product on average, so its
+# algorithmic ceiling is the dense f16 peak / 3.5.
+SPLIT_F16_PRODUCTS = 3.5
+SPLIT_PEAK_TFLOPS = F16_MFMA_PEAK_TFLOPS / SPLIT_F16_PRODUCTS
 N_HEADS, N_KV = 8, 1
 EPS = 1e-6
 LOCAL_BASE, GLOBAL_BASE = 10000.0, 1000000.0
@@ -250,6 +256,7 @@ def bench_prefill(ctx, torch, prep, steps, warmup, N=2048, want_host=False):
         del K, V, q, out
     res["both_layers_us"] = total_s * 1e6
     res["both_layers_tflops"] = total_flops / total_s / 1e12
+    res["frac_of_split_f16_peak"] = res["both_layers_tflops"] / SPLIT_PEAK_TFLOPS
     res["frac_of_f32_mfma_peak"] = res["both_layers_tflops"] / F32_MFMA_PEAK_TFLOPS
     if want_host:
         res["host"] = host
@@ -418,6 +425,7 @@ def floors_lib():
     lib = ctypes.CDLL(path)
     lib.g4f_empty.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
     lib.g4f_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    lib.g4f_mfma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
     return lib
 
 
@@ -446,6 +454,22 @@ def bench_floors(torch, steps, warmup):
                                                                   sink.data_ptr(), 2048, stream())), steps, warmup)
         res[name] = {"us": ev / steps * 1e6, "gbs": nbytes / (ev / steps) / 1e9}
         del bufs
+    # Matrix-pipe rate: two independent accumulator chains per wave, 1 or 2
+    # waves per SIMD (the prefill kernels run 2); cycles per MFMA per SIMD at
+    # the 2.4 GHz peak clock.
+    iters = 4096
+    msink = torch.zeros(512 * 256, device="cuda")
+    for name, f16, flop in (("mfma_16x16x32_f16", 1, 16384), ("mfma_16x16x4_f32", 0, 2048)):
+        for wps in (1, 2):
+            grid = 256 * wps
+            wall, ev = time_steps(torch, lambda i: check(lib.g4f_mfma(f16, grid, iters, msink.data_ptr(), stream())),
+                                  max(1, steps // 10), max(1, warmup // 10))
+            s = ev / max(1, steps // 10)
+            per_simd = wps * 2 * iters
+            res[f"{name}_{wps}_waves_per_simd"] = {
+                "us": s * 1e6, "cycles_per_mfma_at_2400mhz": s * 2.4e9 / per_simd,
+                "tflops": grid * 4 * 2 * iters * flop / s / 1e12}
+    del msink
     torch.cuda.empty_cache()
     return res
 
@@ -752,12 +776,18 @@ def main():
             "global_d512": {k2: round(v, 3) for k2, v in c4["global_d512"].items()},
             "both_layers_us": round(c4["both_layers_us"], 2),
             "roofline": {"bound": "mfma", "achieved": round(c4["both_layers_tflops"], 2),
-                         "peak": F32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                         "frac": round(c4["frac_of_f32_mfma_peak"], 4),
+                         "peak": round(SPLIT_PEAK_TFLOPS, 2), "unit": "TFLOP/s",
+                         "frac": round(c4["frac_of_split_f16_peak"], 4),
+                         "peak_note": "dense f16 MFMA peak 2500 TFLOP/s / 3.5 f16 products per counted product "
+                                      "(3 per score, 4 per weight x value); counted FLOPs = 4 x 8 heads x d per "
+                                      "attended pair",
+                         "frac_of_f32_mfma_peak": round(c4["frac_of_f32_mfma_peak"], 4),
                          "traffic": traffic_bytes("prefill_2048_sliding_and_global.txt"),
-                         "traffic_note": "HBM bytes of one step (both layers' prefill and merge launches) from "
-                                         "the rocprofv3 FETCH_SIZE / WRITE_SIZE passes in profiles/",
-                         "dtype": "f32 MFMA (v_mfma_f32_16x16x4f32)",
+                         "traffic_note": "HBM bytes of one step (both layers' K/V split, prefill and merge "
+                                         "launches) from the rocprofv3 FETCH_SIZE / WRITE_SIZE passes in profiles/",
+                         "dtype": "f32 in and out; products as split-f16 MFMAs (v_mfma_f32_16x16x32_f16 on f16 hi "
+                                  "+ lo halves of each operand), f32 accumulation; units whose inputs the split "
+                                  "does not carry use v_mfma_f32_16x16x4f32",
                          "mfma_busy_counter": {k2: v["mfma_busy"] for k2, v in mfma.items()} or None,
                          "mfma_source": "profiles/prefill_2048_sliding_and_global.txt (SQ_VALU_MFMA_BUSY_CYCLES)"},
             "cpu_baseline": cpu.get("4")},
