@@ -108,6 +108,29 @@ def test_out_of_range_kv_values(ctx, d, window, value):
     assert not np.array_equal(split[:288], exact[:288])
 
 
+def test_blocks_mixing_split_and_f32_units_merge_alike(ctx):
+    """2048-token global prompt with one K value of 40000 in tile 62 (rows
+    992..1007): the units that read that tile run in f32, the other units of
+    the same position blocks in the split form, and the merge combines both
+    kinds of partial (the split form's weights carry 2^7, which its partials
+    fold into m).  Every row against the oracle."""
+    import g4hip
+    d, window, N, tile = 512, 0, 2048, 62
+    units, _ = g4hip.prefill_schedule(0, N, window, d, 1, 256)
+    by_block = {}
+    for b, lo, hi, _slot in units:
+        by_block.setdefault(int(b), []).append((int(lo), int(hi)))
+    mixed = [b for b, us in by_block.items()
+             if len(us) > 1 and any(lo <= tile < hi for lo, hi in us) and any(not lo <= tile < hi for lo, hi in us)]
+    assert mixed, "the schedule no longer splits long blocks"
+    q, K, V = case(8500, N, d)
+    K[16 * tile + 5, 100] = 40000.0
+    split = run(ctx, q, K, V, 0, N, window, d, 0)
+    w = worst_vs_oracle(split, q, K, V, 0, window)
+    print(f"[parity] {len(mixed)} mixed blocks; worst {w:.2e}", flush=True)
+    assert w <= TOL
+
+
 @pytest.mark.parametrize("d,window", [(256, 512), (512, 0)])
 def test_small_q_and_k(ctx, d, window):
     """q and K scaled by 2^-10: about one element in twenty has a subnormal
