@@ -428,9 +428,15 @@ __device__ __forceinline__ bool prefill_unit(const PrefillK &p, const PrefillUni
     // The split form issues its first tiles before it knows whether it will
     // use them, so that their latency overlaps the q loads and the check.
     if constexpr (SPLIT16) {
+        // K(0), V(0) and K(1): the split form's step loop reads K one step
+        // ahead of V.
 #pragma unroll
-        for (int j = 0; j < TPS; ++j)
+        for (int j = 0; j < TPS; ++j) {
             issue_tile(u.t_lo + j < u.t_hi ? u.t_lo + j : u.t_hi - 1, lds_k0 + j * TILE_F4, lds_v0 + j * TILE_F4);
+            const int t1 = u.t_lo + TPS + j < u.t_hi ? u.t_lo + TPS + j : u.t_hi - 1;
+#pragma unroll
+            for (int e = 0; e < PER_THREAD; ++e) issue_part(t1, 2 * e, lds_k1 + j * TILE_F4, nullptr);
+        }
     }
 
     // Q^T (B operand): lane (g, c) holds q[row c][d0 + 32u + 8g + j].
@@ -754,11 +760,7 @@ __device__ __forceinline__ bool prefill_unit(const PrefillK &p, const PrefillUni
             }
             return a0 + (a1 + a2) * kLoUnscale;
         };
-        // K(1); K(0) and V(0) were issued at the unit's start.
-#pragma unroll
-        for (int j = 0; j < TPS; ++j)
-#pragma unroll
-            for (int e = 0; e < PER_THREAD; ++e) issue_part(tile_at(1, j), 2 * e, lds_k1 + j * TILE_F4, nullptr);
+        // K(0), V(0) and K(1) were issued at the unit's start.
         __builtin_amdgcn_s_waitcnt(kVmcntZero);
         __syncthreads();  // K(0), V(0), K(1) have landed
         f32x4 sc_next;    // D = 256: the wave's own scores of the next step
