@@ -161,7 +161,6 @@ struct SplitK {
     int64_t kv_origin;
     int64_t row_lo, row_hi;
     int64_t t0;
-    int n_tiles;
     _Float16 *planes;
     int *tile_flags;
 };
@@ -1529,7 +1528,6 @@ int launch_prefill(g4_ctx *ctx, const PrefillArgs &a, hipStream_t stream) {
         s.row_lo = row_lo;
         s.row_hi = row_hi;
         s.t0 = t0;
-        s.n_tiles = (int)n_tiles;
         s.planes = (_Float16 *)p.planes;
         s.tile_flags = (int *)p.tile_flags;
         const dim3 sg((unsigned)n_tiles, (unsigned)a.n_kv_heads, 2);
