@@ -22,8 +22,9 @@ CPU baseline: 1 sliding decode over 64 keys, 2 global decode over 4096 keys
 (HBM-cold: K/V copies rotated), 3 the 35-layer E2B stack at context 8192
 (cold and resident), 4 a 2048-token prefill through a sliding and a global
 layer (MFMA-bound), 5 the ragged batch.  `workloads` adds the layer drivers
-with their fused input preparation, the Q8_0 mat-vecs and the launch and
-streaming-read floors.  HBM byte counters come from the committed rocprofv3
+with their fused input preparation, chunked prompts deep into a long context
+(split-f16 and f32 products), the Q8_0 mat-vecs and the launch,
+streaming-read and matrix-pipe floors.  HBM byte counters come from the committed rocprofv3
 summaries under profiles/.
 """
 import argparse
@@ -260,6 +261,36 @@ def bench_prefill(ctx, torch, prep, steps, warmup, N=2048, want_host=False):
     res["frac_of_f32_mfma_peak"] = res["both_layers_tflops"] / F32_MFMA_PEAK_TFLOPS
     if want_host:
         res["host"] = host
+    return res
+
+
+def bench_prefill_chunks(ctx, torch, prep, steps, warmup):
+    """Chunked prompts deep into a long context on a global layer (d=512):
+    256 tokens at position 16384 and 2048 tokens at position 30720, each in
+    the split-f16 form (the default) and with f32 MFMA products only
+    (g4_set_prefill_exact), FLOPs counted as for configuration 4."""
+    res = {}
+    try:
+        for name, d, window, pos0, N in (("global_d512_chunk256_at16384", 512, 0, 16384, 256),
+                                         ("global_d512_chunk2048_at30720", 512, 0, 30720, 2048)):
+            K = prep.rows(pos0 + N, d, 0, GLOBAL_BASE, prep.rope_freqs(d))
+            V = prep.rows(pos0 + N, d, 0, 0.0, None, rope=False)
+            q = prep.rows(N, d, pos0, GLOBAL_BASE, prep.rope_freqs(d), heads=N_HEADS)
+            out = torch.zeros(N * N_HEADS * d, device="cuda")
+            fl = sum(4 * N_HEADS * d * (min(p + 1, window) if window else p + 1) for p in range(pos0, pos0 + N))
+            r = {"flops": fl}
+            for form, exact in (("split_f16", 0), ("f32", 1)):
+                ctx.set_prefill_exact(exact)
+                wall, ev = time_steps(torch, lambda i: ctx.attend_prefill(q, K, V, pos0, N, window, N_HEADS, N_KV, d,
+                                                                          out), steps, warmup)
+                ctx.check_status()
+                r[form] = {"us": ev / steps * 1e6, "tflops": fl / (ev / steps) / 1e12,
+                           "frac_of_split_f16_peak": fl / (ev / steps) / 1e12 / SPLIT_PEAK_TFLOPS}
+            res[name] = r
+            del K, V, q, out
+    finally:
+        ctx.set_prefill_exact(0)
+    torch.cuda.empty_cache()
     return res
 
 
@@ -661,7 +692,7 @@ def cpu_ragged(cpu, host, nbytes, seconds):
 
 
 # ------------------------------------------------------------------ main
-ONLY = ["sliding", "global", "stack", "stackwarm", "prefill", "ragged", "layer", "matvec", "floors", "copy"]
+ONLY = ["sliding", "global", "stack", "stackwarm", "prefill", "chunks", "ragged", "layer", "matvec", "floors", "copy"]
 
 
 def run_only(args, torch, g4hip):
@@ -675,6 +706,7 @@ def run_only(args, torch, g4hip):
               "prefill": lambda: bench_prefill(ctx, torch, prep, min(args.steps, 20), args.warmup),
               "ragged": lambda: bench_ragged(ctx, torch, prep, max(5, k // 4), 2),
               "layer": lambda: bench_layer_steps(ctx, torch, prep, args.steps, args.warmup),
+              "chunks": lambda: bench_prefill_chunks(ctx, torch, prep, 10, 3),
               "matvec": lambda: bench_matvec(ctx, torch, max(20, k // 2), args.warmup),
               "floors": lambda: bench_floors(torch, max(20, k), 5),
               "copy": lambda: bench_copy(torch, max(5, k // 4))}[args.only]
@@ -719,6 +751,7 @@ def main():
         c3w = bench_stack(ctx, torch, prep, g4hip, k, 5, cold=False, want_host=want)
         c4 = bench_prefill(ctx, torch, prep, min(steps, 20), warmup, want_host=want)
         workloads = {"layer_drivers": bench_layer_steps(ctx, torch, prep, steps, warmup),
+                     "prefill_long_context": bench_prefill_chunks(ctx, torch, prep, 10, 3),
                      "q8_0_matvec": bench_matvec(ctx, torch, max(20, k // 2), warmup),
                      "floors": bench_floors(torch, k, 5)}
     cpu = {}
