@@ -237,6 +237,8 @@ constexpr int kNonTemporal = 2;
 //   one sequence, 8192 keys d=512:              12.2 -> 11.0 us
 //   ragged batch, 32 sliding windows of 512:    12.9 -> 12.5 us
 // K keeps the default policy; NT on K was slower (351 us on the first).
+// decode_stream_kernel reads K with whole-line loads through LDS instead
+// (KLdsLane), NT like V: the first case then takes 304 us (6.7 TB/s).
 constexpr int kv_policy(int k, int v) { return k | (v << 8); }
 constexpr int kPolicyK(int aux) { return aux & 0xff; }
 constexpr int kPolicyV(int aux) { return (aux >> 8) & 0xff; }
@@ -291,6 +293,13 @@ struct DecodeLane {
         for (int u = 0; u < KU; ++u)
             T.k[u] = __builtin_bit_cast(
                 f32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, koff + toff + 64u * u, 0, kPolicyK(AUX)));
+        load_v<AUX>(vrs, toff, T);
+    }
+
+    // V of the tile at byte offset toff (a multiple of tile_bytes, or an
+    // offset past the resource's range, which reads zeros).
+    template <int AUX>
+    __device__ __forceinline__ void load_v(__amdgpu_buffer_rsrc_t vrs, uint32_t toff, KvTile<D> &T) const {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             if constexpr (TW == 4)
@@ -299,6 +308,41 @@ struct DecodeLane {
                 T.v[r] = __builtin_bit_cast(VRow, __builtin_amdgcn_raw_buffer_load_b64(vrs, voff[r] + toff, 0, kPolicyV(AUX)));
         }
     }
+};
+
+// K through LDS (decode_stream_kernel).  A lane's K load above covers half
+// of each 128-byte line it touches (the A operand puts one key in 16
+// lanes' reach of 64 bytes), and that pattern streams at ~6.0 TB/s against
+// ~7.0 for whole lines.  Here a tile's K slice of one wave (16 keys x DW
+// dims, QPK 16-byte quads per key) arrives by KU LDS-DMA loads: load u
+// takes, in lane L, quad (L % QPK) ^ sw(k) of key k = KPI*u + L / QPK --
+// each load reads whole lines, non-temporally -- and writes LDS slot
+// 64u + L.  The operand of lane (g, c), group u' (key c, quad 4u' + g) is
+// then at slot 64(c / KPI) + QPK(c % KPI) + ((4u' + g) ^ sw(c)); the
+// swizzle sw puts the keys that 8 or 16 lanes of a read name on distinct
+// 16-byte bank groups.
+template <int D>
+struct KLdsLane {
+    static constexpr int DW = DecodeShape<D>::DW, KU = DecodeShape<D>::KU;
+    static constexpr int QPK = DW / 4;   // quads per key: 16 or 8
+    static constexpr int KPI = 64 / QPK;  // keys per load: 4 or 8
+    static_assert(KPI * KU == 16, "a tile's 16 keys in KU loads");
+    __device__ __forceinline__ static int sw(int k) { return QPK == 16 ? k : ((k >> 1) ^ ((k & 1) << 2)); }
+    uint32_t off[KU];  // byte offset of load u within a tile
+    int rd[KU];        // slot of group u's operand
+
+    __device__ __forceinline__ KLdsLane(const DecodeLane<D> &ln, int stride) {
+#pragma unroll
+        for (int u = 0; u < KU; ++u) {
+            const int k = KPI * u + ln.lane / QPK;
+            off[u] = (uint32_t)(k * stride + 4 * ((ln.lane % QPK) ^ sw(k))) * 4u;
+            rd[u] = 64 * (ln.c / KPI) + QPK * (ln.c % KPI) + ((4 * u + ln.g) ^ sw(ln.c));
+        }
+    }
+};
+
+struct NoHook {
+    __device__ __forceinline__ void operator()() const {}
 };
 
 // Partial S^T of a pair, double-buffered: [buffer][tile][wave][lane].
@@ -341,9 +385,14 @@ struct DecodeAcc {
     // chains of a pair run together, so each fixed latency -- the barrier,
     // the LDS round trip, the softmax's dependent steps -- is paid once per
     // 32 keys.  NT = 1: only the first tile (a split of at most 16 keys).
-    template <int NT = 2>
+    // after_exchange runs once every wave has passed the exchange barrier
+    // (so this wave's reads of the pair's K operands have completed) and
+    // this wave has issued its reads of the exchanged scores -- the last LDS
+    // reads of the pair.
+    template <int NT = 2, typename Hook = NoHook>
     __device__ __forceinline__ void pair(const L &ln, const KvTile<D> &P0, const KvTile<D> &P1, int valid,
-                                         float scale, PairScores<D> &sx, int &buf) {
+                                         float scale, PairScores<D> &sx, int &buf,
+                                         const Hook &after_exchange = Hook()) {
         const KvTile<D> *P[2] = {&P0, &P1};
         // Partial S^T of both tiles over this wave's dims (two MFMA chains).
         f32x4 acc[2] = {};
@@ -373,6 +422,7 @@ struct DecodeAcc {
                 sc[t] = (v[0] + v[1]) + (v[2] + v[3]);
         }
         buf ^= 1;
+        after_exchange();
 
         // Scores of keys 16t + 4g + r of the pair for head c; NaN or +inf
         // fails the call; keys past the end (a last pair) are masked.
@@ -542,6 +592,88 @@ __device__ __forceinline__ void run_pairs(const DecodeLane<D> &ln, DecodeAcc<D> 
     }
     pp.prime(ln, krs, vrs, q_first, n_pairs);
     pp.finish(ln, acc, krs, vrs, q_first, n_pairs, n_keys, scale, sx, buf);
+}
+
+// One 16-byte load per lane from `rsrc` at byte offset voff (the range check
+// covers it), written straight to LDS at lds + 16 * lane (lds is the same for
+// the whole wavefront).
+template <int POLICY>
+__device__ __forceinline__ void load_to_lds(__amdgpu_buffer_rsrc_t rsrc, f32x4 *lds, uint32_t voff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void *)lds, 16, voff, 0, 0,
+                                             POLICY);
+#endif
+}
+
+// Tile offset of the loads past a run's last pair: beyond every resource's
+// range (the stream kernel's ranges span < 2^31 bytes, and 2^31 plus a
+// pair's tile and per-lane offsets, < 128 rows of stride, does not wrap), so
+// they read zeros without touching memory while the loads themselves stay
+// unconditional -- which keeps the compiler's wait counts exact.
+constexpr uint32_t kPastEnd = 0x80000000u;
+
+// run_pairs with K through LDS (KLdsLane; lk = this wave's two tile slices,
+// [2 * KU][64] slots) and V through two register slots.  Pair i's V is
+// fetched one pair ahead, at the top of pair i-1; its K once pair i-1's
+// scores have been exchanged (after the last LDS read of pair i-1's K, and
+// after the pair's other LDS reads, which the compiler would otherwise hold
+// until the K transfer lands), so one LDS slice serves every pair.  Each
+// pair waits for its K and V behind the next pair's V loads.
+template <int D, int AUX>
+__device__ __forceinline__ void run_pairs_ldsk(const DecodeLane<D> &ln, const KLdsLane<D> &kl, f32x4 (*lk)[64],
+                                               DecodeAcc<D> &acc, __amdgpu_buffer_rsrc_t krs,
+                                               __amdgpu_buffer_rsrc_t vrs, int q_first, int n_pairs, int n_keys,
+                                               float scale, PairScores<D> &sx, int &buf) {
+    constexpr int KU = DecodeShape<D>::KU;
+    if (n_keys - 32 * q_first <= 16) {  // a single tile, through registers as run_pairs does
+        KvTile<D> T;
+        ln.template load_tile<AUX>(krs, vrs, 2 * q_first, T);
+        acc.template pair<1>(ln, T, T, n_keys - 32 * q_first, scale, sx, buf);
+        return;
+    }
+    auto pair_off = [&](int i) {  // byte offset of pair i of the run
+        return i < n_pairs ? (uint32_t)(2 * (q_first + i)) * ln.tile_bytes : kPastEnd;
+    };
+    auto fetch_k = [&](uint32_t off) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int u = 0; u < KU; ++u)
+                load_to_lds<kPolicyV(AUX)>(krs, lk[t * KU + u], kl.off[u] + off + t * ln.tile_bytes);
+    };
+    auto fetch_v = [&](uint32_t off, KvTile<D>(&P)[2]) {
+        ln.template load_v<AUX>(vrs, off, P[0]);
+        ln.template load_v<AUX>(vrs, off + ln.tile_bytes, P[1]);
+    };
+    // Pair i from cur (its V), with the next pair's V into nxt.
+    auto step = [&](int i, KvTile<D>(&cur)[2], KvTile<D>(&nxt)[2]) {
+        const uint32_t next = pair_off(i + 1);
+        fetch_v(next, nxt);
+        // Pair i's K (LDS) and V have landed once at most the 8 V loads just
+        // issued are outstanding (loads complete in order).
+        asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const f32x4 *tile = lk[t * KU];  // the tile's 64 * KU slots
+#pragma unroll
+            for (int u = 0; u < KU; ++u) cur[t].k[u] = tile[kl.rd[u]];
+        }
+        acc.pair(ln, cur[0], cur[1], n_keys - 32 * (q_first + i), scale, sx, buf, [&] {
+            __builtin_amdgcn_sched_barrier(0);
+            fetch_k(next);
+        });
+    };
+    // V before K, the order in which the steps issue them.
+    KvTile<D> T[2][2];
+    fetch_v(pair_off(0), T[0]);
+    fetch_k(pair_off(0));
+    for (int i = 0; i < n_pairs; i += 2) {
+        step(i, T[0], T[1]);
+        if (i + 1 < n_pairs) step(i + 1, T[1], T[0]);
+    }
+    // The run's last K transfer (past the end) writes this wave's slice;
+    // let it land before the next run, or the workgroup's end, reuses it.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 // One workgroup = one (split, KV head, sequence); NW wavefronts, each owning
@@ -744,10 +876,11 @@ __device__ inline int stream_plan(const DecodeK &p, int *pref, int64_t *first_ro
     return pref[B];
 }
 
-template <int D, int NBUF>
+template <int D>
 __global__ __launch_bounds__(64 * DecodeShape<D>::NW) void decode_stream_kernel(DecodeK p) {
     const int w = blockIdx.x, W = gridDim.x, kvh = blockIdx.y;
     const DecodeLane<D> ln((int)p.row_stride);
+    const KLdsLane<D> kl(ln, (int)p.row_stride);
     const int B = p.n_seqs, G = p.group, stride = (int)p.row_stride;
     __shared__ int pref[kStreamMaxSeqs + 1];
     __shared__ int64_t first_row[kStreamMaxSeqs];
@@ -776,6 +909,8 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::NW) void decode_stream_kernel(
     };
 
     __shared__ PairScores<D> sx;
+    // Each wave's K slices of a pair (KLdsLane): 64 KiB at D = 512.
+    __shared__ f32x4 lk[DecodeShape<D>::NW][2 * DecodeShape<D>::KU][64];
     int buf = 0;
     DecodeAcc<D> acc;
     acc.bad = false;
@@ -789,7 +924,7 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::NW) void decode_stream_kernel(
         const __amdgpu_buffer_rsrc_t krs = ln.rows(p.k + first, n_keys, stride);
         const __amdgpu_buffer_rsrc_t vrs = ln.rows(p.v + first, n_keys, stride);
         acc.start(ln, p.q + ((int64_t)cs * p.n_heads + head) * D);
-        run_pairs<D, NBUF, kKvPolicy>(ln, acc, krs, vrs, g - ga, ge - g, n_keys, p.scale, sx, buf);
+        run_pairs_ldsk<D, kKvPolicy>(ln, kl, lk[ln.wave], acc, krs, vrs, g - ga, ge - g, n_keys, p.scale, sx, buf);
         if (g == ga && ge == gb) {
             acc.write_output(ln, p.out + ((int64_t)cs * p.n_heads + head) * D, col_valid, p.status);
         } else {  // slot 0: the run's first sequence; 1: its last
@@ -997,11 +1132,9 @@ int launch_stream(g4_ctx *ctx, const DecodeArgs &a, DecodeK p, hipStream_t strea
     p.n_seqs = a.B;
     const dim3 grid((unsigned)W, (unsigned)a.n_kv_heads);
     if (D == 256)
-        hipLaunchKernelGGL((decode_stream_kernel<256, kDecodeBuffers>), grid, dim3(64 * DecodeShape<256>::NW), 0,
-                           stream, p);
+        hipLaunchKernelGGL((decode_stream_kernel<256>), grid, dim3(64 * DecodeShape<256>::NW), 0, stream, p);
     else
-        hipLaunchKernelGGL((decode_stream_kernel<512, kDecodeBuffers>), grid, dim3(64 * DecodeShape<512>::NW), 0,
-                           stream, p);
+        hipLaunchKernelGGL((decode_stream_kernel<512>), grid, dim3(64 * DecodeShape<512>::NW), 0, stream, p);
     G4_HIP(hipGetLastError());
     const dim3 mgrid(D * G / 64, a.n_kv_heads, a.B);
     if (D == 256)
