@@ -37,6 +37,8 @@ PREP_CASES = [
     (512, 8, 1, True, 1, 4095),
     (512, 8, 1, True, 37, 100),
     (256, 8, 1, False, 300, 0),
+    (512, 8, 1, True, 301, 5000),  # a prompt chunk (several tokens per workgroup), ragged last group
+    (256, 4, 1, False, 67, 0),     # 6 head rows per token
     (16, 4, 2, True, 5, 0),
     (8, 4, 2, False, 3, 7),
     (128, 16, 2, True, 2, 32767),
