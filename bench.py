@@ -54,6 +54,10 @@ WINDOW = 512
 MALL_BYTES = 256 << 20
 RAGGED_SEED, RAGGED_B = 2024, 32
 METRIC = "decode-attn µs/layer + achieved HBM GB/s; prefill-attn TFLOP/s (1× MI355X)"
+# How the timed CPU restatement is built (oracle/Makefile); the GPU host's
+# AVX2 level stands in for -march=native, since the library is built
+# elsewhere and shipped to that host.
+ORACLE_BUILD = "gcc -O3 -march=x86-64-v3 -ffp-contract=off -fno-fast-math (oracle/Makefile)"
 
 
 def decode_bytes(rows, d):
@@ -103,14 +107,23 @@ class Prep:
         return self.torch.rand(d // 2, device="cuda", generator=self.gen) * 7.0 + 1.0
 
 
-def time_steps(torch, fn, steps, warmup):
-    """Runs `warmup` eager steps, captures the `steps` timed steps into one
-    HIP graph and times one replay of it between synchronisations, with HIP
-    events on the current stream (where fn(i) launches step i) and with the
-    host clock.  Returns (wall seconds, event seconds) for the `steps`
-    steps."""
-    for i in range(warmup):
+WARM_SECONDS = 0.1
+
+
+def time_steps(torch, fn, steps, warmup, warm_seconds=WARM_SECONDS):
+    """Runs at least `warmup` eager steps and at least `warm_seconds` of them
+    (the clocks need tens of milliseconds of a load to settle: a step timed
+    after a handful of warm-up calls reads slow), captures the `steps` timed
+    steps into one HIP graph and times one replay of it between
+    synchronisations, with HIP events on the current stream (where fn(i)
+    launches step i) and with the host clock.  Returns (wall seconds, event
+    seconds) for the `steps` steps."""
+    t0, i = time.perf_counter(), 0
+    while i < warmup or time.perf_counter() - t0 < warm_seconds:
         fn(i)
+        i += 1
+        if i >= warmup and i % 8 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
@@ -227,6 +240,66 @@ def bench_stack(ctx, torch, prep, g4hip, steps, warmup, ctx_len=8192, cold=True,
         res["host"] = {"plan": plan, "q": [q.cpu().numpy() for q in qs],
                        "kv": {l: (K.cpu().numpy(), V.cpu().numpy()) for l, (K, V) in caches[0].items()}}
     return res
+
+
+def bench_layer_stack(ctx, torch, prep, g4hip, steps, warmup, ctx_len=8192, want_host=False):
+    """The per-token attention segment of the whole E2B stack as the engine
+    runs it through the layer driver: one g4_layer_attention call per layer
+    (model.rs:394-410: q norm + RoPE; on the 15 owner layers the new row's
+    k/v norm + RoPE and its append; the view and window; attention), 35
+    calls per token, each one fused launch plus the split merge.  Owners
+    start with ctx_len - 1 rows; every step decodes the next token (the
+    caches grow by one row per step: the timed steps sit at contexts
+    ctx_len + warm-up steps onward).  q, k and v are raw (pre-norm) draws,
+    the norm weights ones, the global layers' RoPE factors E2B's
+    proportional ones."""
+    hp = g4hip.G4Hparams.e2b()
+    plan = stack_plan(g4hip, ctx_len)
+    extra = 8192  # rows of room for warm-up and timed steps
+    widths = [d if src == layer else 0 for (layer, src, b, e, d, glob) in plan]
+    cache = g4hip.KvCache(ctx, widths, ctx_len + extra)
+    host = {}
+    try:
+        freqs = torch.tensor(g4hip.proportional_rope_freq_factors(512, 0.25), device="cuda")
+        for layer, src, b, e, d, glob in plan:
+            if src == layer:
+                K = prep.rows(ctx_len - 1, d, 0, GLOBAL_BASE if glob else LOCAL_BASE, freqs if glob else None)
+                V = prep.rows(ctx_len - 1, d, 0, 0.0, None, rope=False)
+                cache.append_rows(layer, K, V, ctx_len - 1)
+                if want_host:
+                    host[layer] = (K.cpu().numpy(), V.cpu().numpy())
+                del K, V
+        qs = [prep.randn(N_HEADS * d) for (layer, src, b, e, d, glob) in plan]
+        ks = [prep.randn(N_KV * d) for (layer, src, b, e, d, glob) in plan]
+        vs = [prep.randn(N_KV * d) for (layer, src, b, e, d, glob) in plan]
+        ones = {256: torch.ones(256, device="cuda"), 512: torch.ones(512, device="cuda")}
+        outs = [torch.zeros(N_HEADS * d, device="cuda") for (layer, src, b, e, d, glob) in plan]
+        state = {"pos": ctx_len - 1}
+
+        def step(i):
+            pos = state["pos"]
+            for (layer, src, b, e, d, glob), q, k, v, out in zip(plan, qs, ks, vs, outs):
+                cache.layer_attention(hp, layer, pos, q, k, v, ones[d], ones[d], freqs, out)
+            state["pos"] = pos + 1
+
+        first = state["pos"]
+        wall, ev = time_steps(torch, step, steps, warmup, warm_seconds=0.05)
+        ctx.check_status()
+        timed_from = state["pos"] - steps
+        res = {"us_per_token": ev / steps * 1e6, "wall_us_per_token": wall / steps * 1e6,
+               "us_per_layer_mean": ev / steps / len(plan) * 1e6, "layers": len(plan),
+               "contexts": [timed_from + 1, timed_from + steps],
+               "note": "35 g4_layer_attention calls per token (fused preparation + append + attention, then the "
+                       "split merge); owners' K/V resident; warm-up steps from context "
+                       f"{first + 1}, timed steps at the contexts given"}
+        if want_host:
+            res["host"] = {"plan": plan, "kv": host, "ctx_len": ctx_len,
+                           "q": [q.cpu().numpy() for q in qs], "k": [k.cpu().numpy() for k in ks],
+                           "v": [v.cpu().numpy() for v in vs], "freqs": freqs.cpu().numpy()}
+        return res
+    finally:
+        cache.close()
+        torch.cuda.empty_cache()
 
 
 def bench_prefill(ctx, torch, prep, steps, warmup, N=2048, want_host=False):
@@ -457,6 +530,7 @@ def floors_lib():
     lib.g4f_empty.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
     lib.g4f_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
     lib.g4f_mfma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    lib.g4f_lds_mfma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
     return lib
 
 
@@ -500,6 +574,27 @@ def bench_floors(torch, steps, warmup):
             res[f"{name}_{wps}_waves_per_simd"] = {
                 "us": s * 1e6, "cycles_per_mfma_at_2400mhz": s * 2.4e9 / per_simd,
                 "tflops": grid * 4 * 2 * iters * flop / s / 1e12}
+    # The pipe fed from LDS: one 1 KiB operand (16 bytes per lane) read per
+    # one or two MFMAs, 16x16x32 (16 cycles of matrix work per instruction at
+    # peak) or 32x32x16 (32); four accumulators per wave.  A 16x16x32 fed one
+    # operand per instruction needs 256 B/clk of LDS per CU at peak.
+    lsteps = max(1, steps // 10)
+    for mode, (shape, mpr) in enumerate((("16x16x32", 0), ("16x16x32", 1), ("16x16x32", 2), ("32x32x16", 0),
+                                         ("32x32x16", 1), ("32x32x16", 2))):
+        flop = 16384 if shape == "16x16x32" else 32768
+        for wps in (1, 2):
+            grid = 256 * wps
+            lit = 1024
+            wall, ev = time_steps(torch, lambda i: check(lib.g4f_lds_mfma(mode, grid, lit, msink.data_ptr(),
+                                                                          stream())), lsteps, 1)
+            s = ev / lsteps
+            per_simd = wps * 8 * lit * max(mpr, 1)
+            cyc = s * 2.4e9 / per_simd
+            r = {"us": round(s * 1e6, 2), "cycles_per_mfma_at_2400mhz": round(cyc, 2),
+                 "tflops": round(grid * 4 * 8 * lit * max(mpr, 1) * flop / s / 1e12, 1)}
+            if mpr:
+                r["lds_bytes_per_clk_per_cu"] = round(4 * wps * 8 * lit * 1024 / (s * 2.4e9), 1)
+            res[f"lds_fed_mfma_{shape}_{mpr}_per_read_{wps}_waves_per_simd"] = r
     del msink
     torch.cuda.empty_cache()
     return res
@@ -577,6 +672,68 @@ def traffic_bytes(name, kernels=None):
     return int(total) if found else None
 
 
+def summarize(base, fetch_scale=2.0, write_scale=1.0):
+    """The profiles/ tables from rocprofv3 CSV output under `base`:
+    trace/run_kernel_stats.csv (--kernel-trace --stats), fetch/ and write/
+    run_counter_collection.csv (--pmc FETCH_SIZE, --pmc WRITE_SIZE; KiB per
+    dispatch, scaled by a plain copy's reading: FETCH_SIZE counts half the
+    bytes a copy reads, profiles/hbm_counter_calibration.txt) and, when
+    present, mfma/ (--pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_VALU_MFMA_MOPS_F16
+    SQ_BUSY_CYCLES GRBM_GUI_ACTIVE).  Returns the text."""
+    import collections
+    import csv
+
+    def short(k):
+        return k.replace("(anonymous namespace)::", "").split("(")[0]
+
+    def ours(n):
+        return n.startswith("void g4::") or n.startswith("g4::")
+
+    lines = []
+    stats = os.path.join(base, "trace", "run_kernel_stats.csv")
+    avg = {}
+    if os.path.exists(stats):
+        rows = list(csv.DictReader(open(stats)))
+        tot = sum(float(r["TotalDurationNs"]) for r in rows) or 1.0
+        lines.append("  kernel                                                        calls     avg us  share")
+        for r in rows:
+            n = short(r["Name"])
+            avg[n] = float(r["AverageNs"])
+            if ours(n):
+                lines.append(f"  {n:<60} {int(r['Calls']):>6} {float(r['AverageNs']) / 1e3:>10.3f} "
+                             f"{100 * float(r['TotalDurationNs']) / tot:>5.1f}%")
+
+    def counters(sub):
+        path = os.path.join(base, sub, "run_counter_collection.csv")
+        if not os.path.exists(path):
+            return None
+        acc = collections.defaultdict(lambda: collections.defaultdict(list))
+        for r in csv.DictReader(open(path)):
+            n = short(r["Kernel_Name"])
+            if ours(n):
+                acc[n][r["Counter_Name"]].append(float(r["Counter_Value"]))
+        return {n: {c: sum(v) / len(v) for c, v in d.items()} for n, d in acc.items()}
+
+    f, w = counters("fetch"), counters("write")
+    if f is not None and w is not None:
+        lines += ["", "  kernel                                                          read MB  written MB"]
+        for n in f:
+            rd = f[n].get("FETCH_SIZE", 0) * 1024 * fetch_scale / 1e6
+            wr = w.get(n, {}).get("WRITE_SIZE", 0) * 1024 * write_scale / 1e6
+            lines.append(f"  {n:<60} {rd:>10.3f} {wr:>11.3f}")
+    m = counters("mfma")
+    if m:
+        lines += ["", "  kernel                                                        mfma busy  TFLOP/s"]
+        for n, d in m.items():
+            g = d.get("GRBM_GUI_ACTIVE", 0)
+            mops = d.get("SQ_INSTS_VALU_MFMA_MOPS_F16") or d.get("SQ_INSTS_VALU_MFMA_MOPS_F32")
+            if not mops or not g or n not in avg:
+                continue
+            busy = d["SQ_VALU_MFMA_BUSY_CYCLES"] / (g / 8 * 1024)
+            lines.append(f"  {n:<60} {busy:>9.3f} {mops * 512 / (avg[n] * 1e-9) / 1e12:>8.1f}")
+    return "\n".join(lines)
+
+
 # ---------------------------------------------------------- CPU baseline
 class CpuTimer:
     """Times the oracle's attend (the reference's attend with its `concat`
@@ -612,7 +769,7 @@ def cpu_decode(cpu, host, T, nbytes, seconds):
     s, n = cpu.loop(lambda: rows.attend(q, 0, T, N_HEADS, N_KV, out), seconds)
     s1, n1 = cpu.loop(lambda: rows.attend(q, 0, T, N_HEADS, N_KV, out, threads=1), seconds / 2)
     return {"value": round(nbytes / s / 1e9, 4), "unit": "GB/s", "us_per_layer": round(s * 1e6, 1),
-            "cores": cpu.threads, "kind": "port",
+            "cores": cpu.threads, "kind": "port", "build": ORACLE_BUILD,
             "sample": f"{n} calls of the same step; single thread {nbytes / s1 / 1e9:.3f} GB/s "
                       f"({s1 * 1e6:.0f} us/step); host has {os.cpu_count()} logical CPUs"}
 
@@ -631,9 +788,52 @@ def cpu_stack(cpu, host, nbytes, seconds):
 
     s, n = cpu.loop(stack, seconds)
     return {"value": round(nbytes / s / 1e9, 4), "unit": "GB/s", "us_per_stack": round(s * 1e6, 1),
-            "cores": cpu.threads, "kind": "port",
+            "cores": cpu.threads, "kind": "port", "build": ORACLE_BUILD,
             "sample": f"{n} whole stacks (35 attend calls each, resident in host memory); "
                       f"host has {os.cpu_count()} logical CPUs"}
+
+
+def cpu_layer_stack(cpu, host, seconds):
+    """The E2B stack's per-token attention segment on the CPU, as the
+    reference's layer loop runs it (model.rs:394-410): per layer the q (and
+    on owners k, v) norm + RoPE (or_prepare_rows, the oracle's norm_heads and
+    rope_heads), the append into the owner's rows, then attend -- with its
+    `concat` copy and per-head pool -- over the window's rows.  Each step is
+    the next token, as on the GPU."""
+    import numpy as np
+    orc = cpu.orc
+    ctx_len = host["ctx_len"]
+    cap = ctx_len + 4096
+    caches, rows = {}, {}
+    for layer, (K, V) in host["kv"].items():
+        Kc = np.zeros((cap, K.shape[1]), np.float32)
+        Vc = np.zeros((cap, V.shape[1]), np.float32)
+        Kc[:K.shape[0]], Vc[:V.shape[0]] = K, V
+        caches[layer] = (Kc, Vc)
+        rows[layer] = cpu.rows(Kc, Vc)
+    freqs = host["freqs"]
+    ones = {256: np.ones(256, np.float32), 512: np.ones(512, np.float32)}
+    state = {"pos": ctx_len - 1}
+
+    def step():
+        pos = state["pos"]
+        for (layer, src, b, e, d, glob), q0, k0, v0 in zip(host["plan"], host["q"], host["k"], host["v"]):
+            base = GLOBAL_BASE if glob else LOCAL_BASE
+            f = freqs if glob else None
+            q = orc.prepare_rows(q0.reshape(1, -1).copy(), d, ones[d], EPS, pos, base, f)[0]
+            if src == layer:
+                caches[layer][0][pos] = orc.prepare_rows(k0.reshape(1, -1).copy(), d, ones[d], EPS, pos, base, f)[0]
+                caches[layer][1][pos] = orc.prepare_rows(v0.reshape(1, -1).copy(), d, None, EPS, 0, 0.0, None)[0]
+            begin = 0 if glob else max(0, pos + 1 - WINDOW)
+            out = np.zeros(N_HEADS * d, np.float32)
+            rows[src].attend(q, begin, pos + 1, N_HEADS, N_KV, out)
+        state["pos"] = pos + 1
+
+    s, n = cpu.loop(step, seconds, min_calls=1)
+    return {"value": round(s * 1e6, 1), "unit": "us/token", "cores": cpu.threads, "kind": "port",
+            "build": ORACLE_BUILD,
+            "sample": f"{n + 1} consecutive tokens from context {ctx_len} (35 layers each: preparation, append "
+                      f"and attend); host has {os.cpu_count()} logical CPUs"}
 
 
 def cpu_prefill(cpu, host, seconds, stride=8):
@@ -662,7 +862,7 @@ def cpu_prefill(cpu, host, seconds, stride=8):
         tot_fl += fl
         tot_s += s
     return {"value": round(tot_fl / tot_s / 1e12, 6), "unit": "TFLOP/s", "cores": cpu.threads, "kind": "port",
-            "layers": res,
+            "build": ORACLE_BUILD, "layers": res,
             "sample": f"the prompt loop at every {stride}th position (256 of 2048 tokens per layer, their own "
                       f"FLOPs); host has {os.cpu_count()} logical CPUs"}
 
@@ -686,13 +886,14 @@ def cpu_ragged(cpu, host, nbytes, seconds):
 
     s, n = cpu.loop(batch, seconds, min_calls=1)
     return {"value": round(nbytes / s / 1e9, 4), "unit": "GB/s", "us_per_step": round(s * 1e6, 1),
-            "cores": cpu.threads, "kind": "port",
+            "cores": cpu.threads, "kind": "port", "build": ORACLE_BUILD,
             "sample": f"{n} whole steps (64 attend calls: 32 sequences x 2 layers); host has "
                       f"{os.cpu_count()} logical CPUs"}
 
 
 # ------------------------------------------------------------------ main
-ONLY = ["sliding", "global", "stack", "stackwarm", "prefill", "chunks", "ragged", "layer", "matvec", "floors", "copy"]
+ONLY = ["sliding", "global", "stack", "stackwarm", "layerstack", "prefill", "chunks", "ragged", "layer", "matvec",
+        "floors", "copy"]
 
 
 def run_only(args, torch, g4hip):
@@ -703,6 +904,7 @@ def run_only(args, torch, g4hip):
               "global": lambda: bench_global_decode(ctx, torch, prep, args.steps, args.warmup),
               "stack": lambda: bench_stack(ctx, torch, prep, g4hip, k, 5, cold=True),
               "stackwarm": lambda: bench_stack(ctx, torch, prep, g4hip, k, 5, cold=False),
+              "layerstack": lambda: bench_layer_stack(ctx, torch, prep, g4hip, k, 5),
               "prefill": lambda: bench_prefill(ctx, torch, prep, min(args.steps, 20), args.warmup),
               "ragged": lambda: bench_ragged(ctx, torch, prep, max(5, k // 4), 2),
               "layer": lambda: bench_layer_steps(ctx, torch, prep, args.steps, args.warmup),
@@ -726,7 +928,13 @@ def main():
     ap.add_argument("--only", choices=ONLY,
                     help="run one workload alone (for profiling) and print its result; 'copy' is a plain "
                          "256 MiB device copy, the reference point for HBM byte counters")
+    ap.add_argument("--summarize", metavar="DIR",
+                    help="print the profiles/ tables reduced from rocprofv3 CSV output under DIR (trace/, fetch/, "
+                         "write/, mfma/) and exit; needs no GPU")
     args = ap.parse_args()
+    if args.summarize:
+        print(summarize(args.summarize))
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the backend runs on a single MI355X, and no run here uses a second "
               f"(asked for --gpus {args.gpus}).", file=sys.stderr)
@@ -749,6 +957,7 @@ def main():
         c2 = bench_global_decode(ctx, torch, prep, steps, warmup)
         c3 = bench_stack(ctx, torch, prep, g4hip, k, 5, cold=True)
         c3w = bench_stack(ctx, torch, prep, g4hip, k, 5, cold=False, want_host=want)
+        c3l = bench_layer_stack(ctx, torch, prep, g4hip, k, 5, want_host=want)
         c4 = bench_prefill(ctx, torch, prep, min(steps, 20), warmup, want_host=want)
         workloads = {"layer_drivers": bench_layer_steps(ctx, torch, prep, steps, warmup),
                      "prefill_long_context": bench_prefill_chunks(ctx, torch, prep, 10, 3),
@@ -762,9 +971,13 @@ def main():
         cpu["1"] = cpu_decode(timer, c1["host"], 64, c1["bytes"], sec / 2)
         cpu["2"] = cpu_decode(timer, c2["host"], 4096, c2["bytes"], sec)
         cpu["3"] = cpu_stack(timer, c3w["host"], c3w["bytes_per_stack"], sec)
+        cpu["layer_stack"] = cpu_layer_stack(timer, c3l["host"], sec)
         cpu["4"] = cpu_prefill(timer, c4["host"], sec)
-    for r in (c1, c2, c3w, c4, c5):
+    for r in (c1, c2, c3w, c3l, c4, c5):
         r.pop("host", None)
+    c3l["attention_only_stack_us_resident"] = round(c3w["us_per_stack"], 2)
+    c3l["cpu_baseline"] = cpu.get("layer_stack")
+    workloads["layer_drivers"]["e2b_stack_35_layers_ctx8192_layer_attention"] = c3l
 
     # The headline: the ragged batch of 32 sequences, both layers per step.
     step_s = c5["step"]["us"] * 1e-6

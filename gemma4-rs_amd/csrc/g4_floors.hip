@@ -6,10 +6,14 @@
 //    the same 16-byte non-temporal loads the decode kernels use for V;
 //  - a matrix-pipe rate: back-to-back v_mfma_f32_16x16x32_f16 (the split
 //    prefill's instruction) and v_mfma_f32_16x16x4f32 on two independent
-//    accumulators per wave, as many waves per SIMD as asked.
+//    accumulators per wave, as many waves per SIMD as asked;
+//  - the matrix pipe fed from LDS: one 16-byte operand per lane read from
+//    LDS per one or two MFMAs (16x16x32 or 32x32x16 f16), which bounds what
+//    a kernel streaming its operands through LDS can keep busy.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 namespace {
 
@@ -70,6 +74,49 @@ __global__ __launch_bounds__(256) void mfma_kernel(float *sink, int iters) {
     sink[blockIdx.x * 256 + l] = (s[0] + s[1]) + (s[2] + s[3]);
 }
 
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// Matrix pipe fed from LDS: each wave reads one 16-byte A operand per lane
+// (ds_read_b128, the wave's 1 KiB contiguous, so bank-conflict free) from a
+// 32 KiB LDS array and feeds it to MPR MFMAs on four independent
+// accumulators; MPR = 0 keeps one operand in registers (the pipe alone).
+// BIG selects v_mfma_f32_32x32x16_f16 (32 cycles of matrix work per 1 KiB
+// operand) over v_mfma_f32_16x16x32_f16 (16).  Eight operands per round.
+template <bool BIG, int MPR>
+__global__ __launch_bounds__(256) void lds_mfma_kernel(float *sink, int iters) {
+    __shared__ f32x4 buf[2048];
+    for (int i = threadIdx.x; i < 2048; i += 256) buf[i] = f32x4{i * 1e-3f, 1.0f, 0.5f, 0.25f};
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    f16x8 b;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) b[j] = (_Float16)(j * 0.5f);
+    f16x8 a0 = __builtin_bit_cast(f16x8, buf[lane]);
+    typedef typename std::conditional<BIG, f32x16, f32x4>::type acc_t;
+    acc_t c[4] = {};
+    const int off = wave * 64 + lane;
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const f16x8 a = MPR == 0 ? a0 : __builtin_bit_cast(f16x8, buf[(off + (u + 8 * it) * 256) & 2047]);
+#pragma unroll
+            for (int m = 0; m < (MPR == 0 ? 1 : MPR); ++m) {
+                acc_t &cc = c[(u * (MPR == 0 ? 1 : MPR) + m) & 3];
+                if constexpr (BIG)
+                    cc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, cc, 0, 0, 0);
+                else
+                    cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, cc, 0, 0, 0);
+            }
+        }
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int j = 0; j < (BIG ? 16 : 4); ++j) s += c[k][j];
+    sink[blockIdx.x * 256 + threadIdx.x] = s;
+}
+
 }  // namespace
 
 extern "C" {
@@ -100,6 +147,25 @@ int g4f_mfma(int f16, int grid, int iters, float *sink, void *stream) {
         hipLaunchKernelGGL(mfma_kernel<true>, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, sink, iters);
     else
         hipLaunchKernelGGL(mfma_kernel<false>, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, sink, iters);
+    return hipGetLastError() == hipSuccess ? 0 : 1;
+}
+
+// One launch of the LDS-fed matrix-pipe kernel: mode 0..5 = (16x16x32,
+// MPR 0), (16x16x32, 1), (16x16x32, 2), (32x32x16, 0), (32x32x16, 1),
+// (32x32x16, 2); grid workgroups of four waves, 8 * iters operand rounds
+// per wave (8 * iters * max(MPR, 1) MFMAs).  sink holds grid * 256 floats.
+int g4f_lds_mfma(int mode, int grid, int iters, float *sink, void *stream) {
+    if (!sink || grid <= 0 || iters <= 0 || mode < 0 || mode > 5) return 1;
+    hipStream_t st = (hipStream_t)stream;
+    const dim3 g((unsigned)grid), b(256);
+    switch (mode) {
+        case 0: hipLaunchKernelGGL((lds_mfma_kernel<false, 0>), g, b, 0, st, sink, iters); break;
+        case 1: hipLaunchKernelGGL((lds_mfma_kernel<false, 1>), g, b, 0, st, sink, iters); break;
+        case 2: hipLaunchKernelGGL((lds_mfma_kernel<false, 2>), g, b, 0, st, sink, iters); break;
+        case 3: hipLaunchKernelGGL((lds_mfma_kernel<true, 0>), g, b, 0, st, sink, iters); break;
+        case 4: hipLaunchKernelGGL((lds_mfma_kernel<true, 1>), g, b, 0, st, sink, iters); break;
+        default: hipLaunchKernelGGL((lds_mfma_kernel<true, 2>), g, b, 0, st, sink, iters); break;
+    }
     return hipGetLastError() == hipSuccess ? 0 : 1;
 }
 

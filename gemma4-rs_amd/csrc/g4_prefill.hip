@@ -365,6 +365,9 @@ __device__ __forceinline__ bool prefill_unit(const PrefillK &p, const PrefillUni
     f32x4(*const lds_s0)[64] = L.s0;
     f32x4(*const lds_s1)[64] = L.s1;
     int *const nf_tile = L.nf_tile;
+    // A flag of an earlier unit is cleared before this unit's first step
+    // (the caller's barrier between units ordered that unit's last read).
+    if (!SPLIT16 && tid < S::KSPLIT) nf_tile[tid] = 0;
 
     // K/V tiles go straight from memory to LDS (buffer_load ... lds: lane l
     // of a wavefront writes the 16 bytes it loads to LDS base + 16*l), so the
@@ -649,8 +652,6 @@ __device__ __forceinline__ bool prefill_unit(const PrefillK &p, const PrefillUni
                 if (__any(found) && lane == 0) nf_tile[kpar] = tw + 1;
             }
             lds_barrier();  // the sanitized tile and the flag are visible to the group
-            // A flag left by an earlier unit with the same tile index only
-            // costs a fix-up pass that finds nothing.
             fix = !(live && whole) && nf_tile[kpar] == tw + 1;
         }
 
@@ -983,8 +984,12 @@ __global__ __launch_bounds__(PrefillShape<D>::THREADS, 1) void prefill_kernel(Pr
         lds_v1[S::TPS * TILE_F4];
     __shared__ f32x4 lds_s0[S::WAVES][64], lds_s1[S::WAVES][64];
     // Per wave group: 1 + the index of the last edge tile whose V held a
-    // non-finite value (see the unit's step()).
+    // non-finite value (see the unit's step()); 0 = none.  Cleared here and
+    // by each f32-form unit, so that leftover LDS contents never trigger a
+    // fix-up pass; the unit's first barrier orders the clear before any
+    // read.
     __shared__ int nf_tile[S::KSPLIT];
+    if (threadIdx.x < S::KSPLIT) nf_tile[threadIdx.x] = 0;
     const PrefillLds L{lds_k0, lds_v0, lds_k1, lds_v1, lds_s0, lds_s1, nf_tile};
     const int first = p.bin_start[blockIdx.x], end = p.bin_start[blockIdx.x + 1];
     for (int i = first; i < end; ++i) {

@@ -104,9 +104,18 @@ impl HipPort {
 
     /// `attend_decode` with its split partials in a fixed device array of the
     /// library: it allocates nothing, for callers that cannot (graph
-    /// capture, serving loops).  No counterpart in the reference.  Calls that
-    /// overlap on one device race on that array.
-    pub fn attend_decode_noalloc(
+    /// capture, serving loops).  No counterpart in the reference.
+    ///
+    /// # Safety
+    ///
+    /// Every call on one device shares that device's array, whatever the
+    /// context or stream, and the work is queued asynchronously: the caller
+    /// must order all `attend_decode_noalloc` calls on a device (one stream,
+    /// or events between streams), including those of other `HipPort`s and
+    /// of `on_stream` views.  Two calls whose work overlaps on the device
+    /// corrupt each other's partials and return wrong outputs without an
+    /// error.
+    pub unsafe fn attend_decode_noalloc(
         &self,
         q: &DevBuf,
         rows: &KvRows<'_>,

@@ -349,11 +349,96 @@ typedef struct {
     int *status;
     float *out;
     atomic_int failed;
-    size_t index; /* this worker's first query */
+    size_t index; /* this worker's first query (first query group when blocked) */
+    int blocked;  /* or_attend_prefill_blocked: groups of PF_GROUP queries */
+    const size_t *positions; /* blocked: query i's position, or NULL for pos0 + i */
 } prefill_ctx;
+
+/* Query groups of the blocked checker: PF_GROUP consecutive queries walk
+ * their keys together, PF_CHUNK rows at a time, so that a key or value row
+ * is fetched from memory once per group rather than once per query and
+ * head. */
+enum { PF_GROUP = 16, PF_CHUNK = 64 };
+
+/* One group of queries [i0, i1) with or_attend's arithmetic: per query and
+ * head the scores are or_dot_f32 * scale in key order, the weights are
+ * or_softmax_f32 over the query's whole range, and out[d] += p_t * v_t[d]
+ * runs over the keys in order; only the loop nest differs from attend_image
+ * (keys outermost, then queries, then heads), which changes no operation or
+ * its order.  A query with a failing head gets that head's output untouched
+ * and the error, as attend_image leaves it. */
+static void prefill_group(prefill_ctx *w, size_t i0, size_t i1) {
+    const size_t nh = w->n_heads, hd = w->q_len / nh, G = i1 - i0;
+    size_t b[PF_GROUP], e[PF_GROUP], off[PF_GROUP];
+    size_t lo = (size_t)-1, hi = 0, total = 0;
+    for (size_t j = 0; j < G; ++j) {
+        const size_t i = i0 + j, pos = w->positions ? w->positions[i] : w->pos0 + i;
+        if (w->window)
+            or_windowed_len(pos + 1, w->window, &b[j], &e[j]);
+        else
+            b[j] = 0, e[j] = pos + 1;
+        off[j] = total;
+        total += (e[j] - b[j]) * nh;
+        if (b[j] < lo) lo = b[j];
+        if (e[j] > hi) hi = e[j];
+    }
+    float *s = (float *)malloc((total ? total : 1) * sizeof(float));
+    int ok[PF_GROUP * 64]; /* per (query, head); run_prefill admits at most 64 heads */
+    for (size_t t0 = lo; t0 < hi; t0 += PF_CHUNK) {
+        const size_t t1 = t0 + PF_CHUNK < hi ? t0 + PF_CHUNK : hi;
+        for (size_t j = 0; j < G; ++j) {
+            const size_t tb = t0 > b[j] ? t0 : b[j], te = t1 < e[j] ? t1 : e[j], T = e[j] - b[j];
+            for (size_t h = 0; h < nh && tb < te; ++h) {
+                const float *qh = w->q + (i0 + j) * w->q_len + h * hd;
+                const size_t kv = (h * w->n_kv_heads / nh) * hd;
+                float *sc = s + off[j] + h * T;
+                for (size_t t = tb; t < te; ++t)
+                    sc[t - b[j]] = or_dot_f32(qh, w->keys + t * w->width + kv, hd) * w->scale;
+            }
+        }
+    }
+    for (size_t j = 0; j < G; ++j) {
+        const size_t T = e[j] - b[j];
+        for (size_t h = 0; h < nh; ++h) {
+            float *sc = s + off[j] + h * T;
+            ok[j * 64 + h] = or_softmax_f32(sc, T, sc) == OR_OK; /* in place: element i is read before written */
+            if (ok[j * 64 + h]) memset(w->out + (i0 + j) * w->q_len + h * hd, 0, hd * sizeof(float));
+        }
+    }
+    for (size_t t0 = lo; t0 < hi; t0 += PF_CHUNK) {
+        const size_t t1 = t0 + PF_CHUNK < hi ? t0 + PF_CHUNK : hi;
+        for (size_t j = 0; j < G; ++j) {
+            const size_t tb = t0 > b[j] ? t0 : b[j], te = t1 < e[j] ? t1 : e[j], T = e[j] - b[j];
+            for (size_t h = 0; h < nh && tb < te; ++h) {
+                if (!ok[j * 64 + h]) continue;
+                const size_t kv = (h * w->n_kv_heads / nh) * hd;
+                const float *pr = s + off[j] + h * T;
+                float *o = w->out + (i0 + j) * w->q_len + h * hd;
+                for (size_t t = tb; t < te; ++t) {
+                    const float p = pr[t - b[j]];
+                    const float *v = w->values + t * w->width + kv;
+                    for (size_t d = 0; d < hd; ++d) o[d] += p * v[d];
+                }
+            }
+        }
+    }
+    for (size_t j = 0; j < G; ++j) {
+        int failed = nh * hd != w->q_len;
+        for (size_t h = 0; h < nh; ++h) failed |= !ok[j * 64 + h];
+        const int rc = failed ? fail(OR_ERR_COMPUTE, "softmax input is not finite") : OR_OK;
+        if (w->status) w->status[i0 + j] = rc;
+        if (failed) atomic_store(&w->failed, 1);
+    }
+    free(s);
+}
 
 static void *prefill_worker(void *arg) {
     prefill_ctx *w = (prefill_ctx *)arg;
+    if (w->blocked) {
+        for (size_t i0 = w->index * PF_GROUP; i0 < w->N; i0 += w->threads * PF_GROUP)
+            prefill_group(w, i0, i0 + PF_GROUP < w->N ? i0 + PF_GROUP : w->N);
+        return NULL;
+    }
     for (size_t i = w->index; i < w->N; i += w->threads) {
         size_t begin, end;
         /* generate.rs:37-41: token i runs as a decode at position pos0 + i. */
@@ -370,13 +455,14 @@ static void *prefill_worker(void *arg) {
     return NULL;
 }
 
-int or_attend_prefill(const float *q, size_t q_len, size_t N, const float *keys, const float *values,
-                      size_t pos0, size_t window, size_t n_heads, size_t n_kv_heads, float scale,
-                      size_t threads, int *status, float *out) {
+static int run_prefill(const float *q, size_t q_len, size_t N, const float *keys, const float *values,
+                       size_t pos0, size_t window, size_t n_heads, size_t n_kv_heads, float scale,
+                       size_t threads, int *status, float *out, int blocked, const size_t *positions) {
     if (n_heads == 0 || threads == 0) return fail(OR_ERR_COMPUTE, "attend_prefill: zero heads or threads");
+    if (blocked && n_heads > 64) return fail(OR_ERR_COMPUTE, "attend_prefill_blocked: more than 64 heads");
     if (threads > 256) threads = 256;
     prefill_ctx base = {q, keys, values, q_len, N, pos0, window, n_heads, n_kv_heads, threads,
-                        n_kv_heads * (q_len / n_heads), scale, status, out, 0, 0};
+                        n_kv_heads * (q_len / n_heads), scale, status, out, 0, 0, blocked, positions};
     prefill_ctx w[256];
     pthread_t th[256];
     for (size_t t = 0; t < threads; ++t) {
@@ -396,6 +482,21 @@ int or_attend_prefill(const float *q, size_t q_len, size_t N, const float *keys,
     }
     for (size_t t = started; t < threads; ++t) failed |= atomic_load(&w[t].failed);
     return failed ? fail(OR_ERR_COMPUTE, "softmax input is not finite") : OR_OK;
+}
+
+int or_attend_prefill(const float *q, size_t q_len, size_t N, const float *keys, const float *values,
+                      size_t pos0, size_t window, size_t n_heads, size_t n_kv_heads, float scale,
+                      size_t threads, int *status, float *out) {
+    return run_prefill(q, q_len, N, keys, values, pos0, window, n_heads, n_kv_heads, scale, threads, status,
+                       out, 0, NULL);
+}
+
+int or_attend_prefill_blocked(const float *q, size_t q_len, size_t N, const size_t *positions,
+                              const float *keys, const float *values, size_t pos0, size_t window,
+                              size_t n_heads, size_t n_kv_heads, float scale, size_t threads, int *status,
+                              float *out) {
+    return run_prefill(q, q_len, N, keys, values, pos0, window, n_heads, n_kv_heads, scale, threads, status,
+                       out, 1, positions);
 }
 
 /* f64 twin: same structure, double throughout (plain sequential sums). */

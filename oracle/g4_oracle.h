@@ -75,6 +75,14 @@ int or_attend_rows(const float *q, size_t q_len, const float *const *key_rows,
 int or_attend_prefill(const float *q, size_t q_len, size_t N, const float *keys, const float *values,
                       size_t pos0, size_t window, size_t n_heads, size_t n_kv_heads, float scale,
                       size_t threads, int *status, float *out);
+/* The same results as or_attend_prefill, bit for bit, from a cache-friendly
+ * loop nest (a checker speed-up for long contexts): groups of consecutive
+ * queries walk their keys together.  positions (NULL: pos0 + i) gives query
+ * i's position, for checking a sample of a chunk's rows.  At most 64 heads. */
+int or_attend_prefill_blocked(const float *q, size_t q_len, size_t N, const size_t *positions,
+                              const float *keys, const float *values, size_t pos0, size_t window,
+                              size_t n_heads, size_t n_kv_heads, float scale, size_t threads, int *status,
+                              float *out);
 /* f64 twin of attend: every product and sum in double, for the noise floor
  * |attend_f32 - attend_f64| that the tolerance policy falls back on. */
 int or_attend_f64(const float *q, size_t q_len, const float *keys, const float *values, size_t T,

@@ -66,6 +66,8 @@ def lib():
                                               c_vp]),
             "or_attend_prefill": (ctypes.c_int, [c_vp, c_size, c_size, c_vp, c_vp, c_size, c_size, c_size, c_size,
                                                  c_f32, c_size, c_vp, c_vp]),
+            "or_attend_prefill_blocked": (ctypes.c_int, [c_vp, c_size, c_size, c_vp, c_vp, c_vp, c_size, c_size,
+                                                         c_size, c_size, c_f32, c_size, c_vp, c_vp]),
             "or_attend_f64": (ctypes.c_int, [c_vp, c_size, c_vp, c_vp, c_size, c_size, c_size, ctypes.c_double,
                                              c_vp]),
             "or_norm_heads": (ctypes.c_int, [c_vp, c_size, c_size, c_vp, c_f32]),
@@ -187,22 +189,36 @@ def attend_rows(q, keys, values, n_heads, n_kv_heads, scale=1.0, threads=0):
     return out
 
 
-def attend_prefill(q, keys, values, pos0, window, n_heads, n_kv_heads, scale=1.0, threads=None):
+def attend_prefill(q, keys, values, pos0, window, n_heads, n_kv_heads, scale=1.0, threads=None, blocked=True,
+                   positions=None):
     """The token-at-a-time prompt loop (generate.rs:37-41): row i of q
     [N, n_heads*head_dim] at position pos0 + i attends rows [b, pos0+i+1) of
     the contiguous keys/values image (row t = position t; b from the window,
     0 = global).  Returns (out [N, q_len], status [N]): status[i] is 0 or the
     oracle's error code for that query; queries run on `threads` OS threads
-    (default: all CPUs)."""
+    (default: all CPUs).  blocked: the same arithmetic with groups of queries
+    walking the keys together (or_attend_prefill_blocked, bit-identical to
+    the plain loop and faster on long contexts).  positions: the rows of q
+    are queries at these positions instead of pos0 + i (a sample of a
+    chunk; blocked form only)."""
     q, keys, values = _f32(q), _f32(keys), _f32(values)
     N, q_len = q.shape
-    if keys.shape[0] < pos0 + N or values.shape[0] < pos0 + N:
-        raise ValueError("keys/values must hold rows up to pos0 + N - 1")
+    last = int(np.max(positions)) + 1 if positions is not None and N else pos0 + N
+    if keys.shape[0] < last or values.shape[0] < last:
+        raise ValueError("keys/values must hold rows up to the last query's position")
     threads = threads or os.cpu_count() or 1
     out = np.zeros((N, q_len), dtype=np.float32)
     status = np.zeros(N, dtype=np.int32)
-    lib().or_attend_prefill(q.ctypes.data, q_len, N, keys.ctypes.data, values.ctypes.data, pos0, window, n_heads,
-                            n_kv_heads, scale, threads, status.ctypes.data, out.ctypes.data)
+    if positions is not None or (blocked and n_heads <= 64):
+        pos = None if positions is None else np.ascontiguousarray(positions, dtype=np.uint64)
+        if pos is not None and pos.shape != (N,):
+            raise ValueError("one position per query row")
+        lib().or_attend_prefill_blocked(q.ctypes.data, q_len, N, None if pos is None else pos.ctypes.data,
+                                        keys.ctypes.data, values.ctypes.data, pos0, window, n_heads, n_kv_heads,
+                                        scale, threads, status.ctypes.data, out.ctypes.data)
+    else:
+        lib().or_attend_prefill(q.ctypes.data, q_len, N, keys.ctypes.data, values.ctypes.data, pos0, window,
+                                n_heads, n_kv_heads, scale, threads, status.ctypes.data, out.ctypes.data)
     return out, status
 
 

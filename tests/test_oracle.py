@@ -297,6 +297,73 @@ def test_attend_prefill_is_the_token_loop(n_heads, n_kv, d, pos0, N, window):
         assert bool(st[i]) == sees, (i, st[i])
 
 
+@pytest.mark.parametrize("n_heads,n_kv,d,pos0,N,window", [(8, 1, 32, 200, 37, 0), (8, 1, 32, 130, 29, 100),
+                                                        (4, 2, 16, 0, 70, 0), (8, 1, 16, 61, 9, 1)])
+def test_blocked_prefill_is_the_token_loop(n_heads, n_kv, d, pos0, N, window):
+    """or_attend_prefill_blocked (the checker's fast loop nest: groups of 4
+    queries walking 64-key chunks together) equals or_attend_prefill bit for
+    bit -- outputs, statuses and the untouched heads of a failing query --
+    on ranges that cross chunk and group edges, on any thread count."""
+    rng = np.random.default_rng(pos0 + 7 * N + window)
+    q = rng.standard_normal((N, n_heads * d)).astype(np.float32)
+    K = rng.standard_normal((pos0 + N, n_kv * d)).astype(np.float32)
+    V = rng.standard_normal((pos0 + N, n_kv * d)).astype(np.float32)
+    ref, st = orc.attend_prefill(q, K, V, pos0, window, n_heads, n_kv, threads=1, blocked=False)
+    for threads in (1, 3):
+        out, st2 = orc.attend_prefill(q, K, V, pos0, window, n_heads, n_kv, threads=threads, blocked=True)
+        assert np.array_equal(out.view(np.uint32), ref.view(np.uint32)) and np.array_equal(st, st2)
+    # A NaN key row and a +inf value row: the same failing queries, the same
+    # bits everywhere else (NaN outputs included).
+    r = pos0 + N // 2
+    Kb, Vb = K.copy(), V.copy()
+    Kb[r, 1] = np.nan
+    Vb[r - 1, 0] = np.inf
+    ref, st = orc.attend_prefill(q, Kb, Vb, pos0, window, n_heads, n_kv, threads=2, blocked=False)
+    out, st2 = orc.attend_prefill(q, Kb, Vb, pos0, window, n_heads, n_kv, threads=2, blocked=True)
+    assert np.array_equal(st, st2) and st.any()
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+    # A sample of the rows at their own positions: the same bits as the chunk.
+    pick = np.arange(1, N, 3)
+    out_s, st_s = orc.attend_prefill(q[pick], Kb, Vb, 0, window, n_heads, n_kv, threads=2, positions=pos0 + pick)
+    assert np.array_equal(st_s, st[pick]) and np.array_equal(out_s.view(np.uint32), ref[pick].view(np.uint32))
+
+
+def test_optimised_build_is_bit_identical(tmp_path):
+    """The shipped oracle (-O3 -march=x86-64-v3, vectorised) gives the same
+    bits as an -O0 build of the same sources: without -ffast-math the
+    compiler may not reassociate a sum or fuse a product, so vectorising
+    the 16-lane dot and the elementwise loops changes no result."""
+    root = os.path.dirname(HERE)
+    so = tmp_path / "liboracle_O0.so"
+    subprocess.run(["gcc", "-O0", "-std=c11", "-fPIC", "-shared", "-ffp-contract=off", "-o", str(so),
+                    os.path.join(root, "oracle", "g4_oracle.c"), os.path.join(root, "oracle", "g4_oracle_matvec.c"),
+                    "-lm", "-lpthread"], check=True)
+    script = """
+import sys, numpy as np
+sys.path.insert(0, sys.argv[1])
+from oracle import pyoracle as orc
+rng = np.random.default_rng(5)
+q = rng.standard_normal((24, 8 * 40)).astype(np.float32)
+K = rng.standard_normal((90, 40)).astype(np.float32)
+V = rng.standard_normal((90, 40)).astype(np.float32)
+x = rng.standard_normal(300).astype(np.float32)
+outs = [orc.attend(q[0], K[:77], V[:77], 8, 1), orc.attend_prefill(q, K, V, 66, 0, 8, 1, threads=2)[0],
+        orc.attend_prefill(q, K, V, 66, 9, 8, 1, threads=2, blocked=False)[0],
+        orc.rms_norm(x, None, 1e-6), orc.rope_neox(x[:64].copy(), 37, 10000.0, 64),
+        np.array([orc.dot_f32(x[:141], x[141:282])], np.float32), orc.softmax_f32(x[:50])]
+np.savez(sys.argv[2], *outs)
+"""
+    res = {}
+    for name, lib in (("O0", str(so)), ("O3", os.path.join(root, "oracle", "liboracle.so"))):
+        npz = tmp_path / f"{name}.npz"
+        subprocess.run([sys.executable, "-c", script, root, str(npz)], env=dict(os.environ, G4_ORACLE_LIB=lib),
+                       check=True)
+        z = np.load(npz)
+        res[name] = [z[k] for k in sorted(z.files, key=lambda f: int(f.split("_")[1]))]
+    for a, b in zip(res["O0"], res["O3"]):
+        assert a.dtype == np.float32 and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
 def test_layer_attention_segment_matches_its_parts():
     """or_layer_attention (model.rs:386-411) equals norm -> rope -> append ->
     view -> window -> attend done by hand, and reports the attended set."""
