@@ -520,14 +520,20 @@ __device__ __forceinline__ bool prefill_unit(const PrefillK &p, const PrefillUni
             const int j = i / (2 * PER_THREAD);
             issue_part(tn[j], i % (2 * PER_THREAD), kn + j * TILE_F4, vn + j * TILE_F4);
         };
-        // Partial S^T over this wave's DH dims: two independent chains.  A
-        // chunk's K operands are read from LDS one chunk ahead, into the other
-        // of two register slots, so the MFMAs of chunk uu run while chunk
-        // uu+1's reads are in flight (one slot made every chunk wait for its
-        // own LDS read).  A group whose tile is stale (the unit's last step
-        // with an odd tile count) only issues its share of the next loads:
-        // its scores are all masked below.
-        f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
+        // Partial S^T over this wave's DH dims: one accumulator per 32-dim
+        // chunk (eight MFMAs of four products each), summed pairwise, so that
+        // a score's f32 rounding grows with the log of the chunk count rather
+        // than with the chunk count (with scores in the hundreds, two long
+        // chains put the form's error at several times that of the
+        // reference's own f32 loop).  A chunk's K operands are read from LDS
+        // one chunk ahead, into the other of two register slots, so the MFMAs
+        // of chunk uu run while chunk uu+1's reads are in flight (one slot
+        // made every chunk wait for its own LDS read).  A group whose tile is
+        // stale (the unit's last step with an odd tile count) only issues its
+        // share of the next loads: its scores are all masked below.
+        f32x4 acc[NU];
+#pragma unroll
+        for (int uu = 0; uu < NU; ++uu) acc[uu] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         if (live) {
             f32x4 kc[2][2];
             auto read_k = [&](int uu, f32x4(&dst)[2]) {
@@ -550,12 +556,11 @@ __device__ __forceinline__ bool prefill_unit(const PrefillK &p, const PrefillUni
                     load(uu / (NU / NL));
                 }
                 const f32x4 k0 = kc[uu & 1][0], k1 = kc[uu & 1][1];
-                f32x4 &acc = (uu & 1) ? acc1 : acc0;
+                f32x4 &a = acc[uu];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k0[j], qreg[uu][j], acc, 0, 0, 0);
+                for (int j = 0; j < 4; ++j) a = __builtin_amdgcn_mfma_f32_16x16x4f32(k0[j], qreg[uu][j], a, 0, 0, 0);
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k1[j], qreg[uu][4 + j], acc, 0, 0, 0);
+                for (int j = 0; j < 4; ++j) a = __builtin_amdgcn_mfma_f32_16x16x4f32(k1[j], qreg[uu][4 + j], a, 0, 0, 0);
             }
             // Scheduling: chunk 0's K reads, then per chunk the next chunk's K
             // reads, the next tile's loads (one or two per 8 MFMAs) and the
@@ -571,7 +576,12 @@ __device__ __forceinline__ bool prefill_unit(const PrefillK &p, const PrefillUni
 #pragma unroll
             for (int i = 0; i < NL; ++i) load(i);
         }
-        f32x4 sc = acc0 + acc1;
+        static_assert((NU & (NU - 1)) == 0, "a power-of-two chunk count");
+#pragma unroll
+        for (int w = 1; w < NU; w *= 2)
+#pragma unroll
+            for (int uu = 0; uu + w < NU; uu += 2 * w) acc[uu] += acc[uu + w];
+        f32x4 sc = acc[0];
         if constexpr (S::SPLIT == 2) {
             // Full scores = half 0 + half 1, added in that order by both waves.
             ls[wave][lane] = sc;
