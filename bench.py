@@ -291,7 +291,8 @@ def bench_layer_stack(ctx, torch, prep, g4hip, steps, warmup, ctx_len=8192, want
                "contexts": [timed_from + 1, timed_from + steps],
                "note": "35 g4_layer_attention calls per token (fused preparation + append + attention, then the "
                        "split merge); owners' K/V resident; warm-up steps from context "
-                       f"{first + 1}, timed steps at the contexts given"}
+                       f"{first + 1}, timed steps at the contexts given",
+               "profile": "profiles/decode_e2b_stack_35_layers_ctx8192_layer_attention.txt"}
         if want_host:
             res["host"] = {"plan": plan, "kv": host, "ctx_len": ctx_len,
                            "q": [q.cpu().numpy() for q in qs], "k": [k.cpu().numpy() for k in ks],

@@ -23,7 +23,8 @@ import bench  # noqa: E402
 
 PROFILES = os.path.join(ROOT, "profiles")
 CITED = ["decode_global_d512_ctx4096.txt", "decode_ragged_b32_ctx1k-32k.txt", "decode_sliding_d256_ctx64.txt",
-         "decode_e2b_stack_35_layers_ctx8192.txt", "prefill_2048_sliding_and_global.txt",
+         "decode_e2b_stack_35_layers_ctx8192.txt", "decode_e2b_stack_35_layers_ctx8192_layer_attention.txt",
+         "prefill_2048_sliding_and_global.txt",
          "q8_0_matvec_output_head_262144x1536.txt", "layer_drivers_global_decode_and_prefill_2048.txt",
          "floors_empty_kernel_and_streaming_read.txt", "hbm_counter_calibration.txt"]
 
