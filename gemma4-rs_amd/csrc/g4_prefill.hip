@@ -1001,7 +1001,13 @@ __global__ __launch_bounds__(PrefillShape<D>::THREADS, 1) void prefill_kernel(Pr
     __shared__ int nf_tile[S::KSPLIT];
     if (threadIdx.x < S::KSPLIT) nf_tile[threadIdx.x] = 0;
     const PrefillLds L{lds_k0, lds_v0, lds_k1, lds_v1, lds_s0, lds_s1, nf_tile};
-    const int first = p.bin_start[blockIdx.x], end = p.bin_start[blockIdx.x + 1];
+    // Workgroups go to the 8 XCDs round-robin (workgroup w to XCD w % 8).
+    // Bin b runs on XCD b / (bins / 8), so that consecutive bins -- the
+    // schedule lists a sliding layer's blocks in position order -- share
+    // one XCD's L2 and the window tiles they have in common.
+    const int gx = gridDim.x;
+    const int bin = gx % 8 == 0 ? (int)(blockIdx.x % 8) * (gx / 8) + (int)(blockIdx.x / 8) : (int)blockIdx.x;
+    const int first = p.bin_start[bin], end = p.bin_start[bin + 1];
     for (int i = first; i < end; ++i) {
         // The previous unit's waves are done with the tile buffers (its
         // spare tile loads landed before its epilogue).
