@@ -540,8 +540,9 @@ def bench_floors(torch, steps, warmup):
     of 256 workgroups x 512 threads (the decode split grid's shape) per
     launch in a captured graph, and streaming reads of 1 MiB (a sliding
     layer's K/V, resident), 16 MiB (a 4096-key global layer's, HBM-cold:
-    copies rotated) and 1 GiB (HBM-cold by size), each one launch of
-    2048 x 256 threads with 16-byte non-temporal loads."""
+    copies rotated), 32 MiB (about the ragged batch's 32 sliding windows,
+    resident in the Infinity Cache) and 1 GiB (HBM-cold by size), each one
+    launch of 2048 x 256 threads with 16-byte non-temporal loads."""
     lib = floors_lib()
 
     def check(rc):
@@ -554,7 +555,7 @@ def bench_floors(torch, steps, warmup):
     res["empty_kernel_256x512"] = {"us_per_launch": ev / steps * 1e6}
     sink = torch.zeros(2048, device="cuda")
     for name, nbytes, copies in (("read_1MiB_resident", 1 << 20, 1), ("read_16MiB_cold", 16 << 20, 24),
-                                 ("read_1GiB", 1 << 30, 1)):
+                                 ("read_32MiB_resident", 32 << 20, 1), ("read_1GiB", 1 << 30, 1)):
         bufs = [torch.ones(nbytes // 4, device="cuda") for _ in range(copies)]
         wall, ev = time_steps(torch, lambda i: check(lib.g4f_read(bufs[i % copies].data_ptr(), nbytes,
                                                                   sink.data_ptr(), 2048, stream())), steps, warmup)
