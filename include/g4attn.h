@@ -62,7 +62,8 @@ int g4_release(g4_ctx *ctx);
  * device-pointer attention calls recorded since the last check, as
  * G4_ERR_COMPUTE "softmax input is not finite" (model.rs:362-364). */
 int g4_check_status(g4_ctx *ctx, g4_stream stream);
-/* Tuning: keys per split-K work item of the decode kernels (0 = automatic). */
+/* Tuning: keys per split-K work item of the decode kernels, rounded up to a
+ * multiple of 16 (0 = automatic). */
 int g4_set_decode_chunk(g4_ctx *ctx, int64_t keys);
 /* Tuning: 1 = prefill computes every product with f32 MFMAs; 0 (default) =
  * split-f16 MFMA products (each f32 operand as an f16 hi + lo pair, three

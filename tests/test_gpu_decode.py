@@ -70,12 +70,14 @@ def test_decode_lengths(ctx, d, T):
     assert I.rel_err(out, orc.attend(q, K, V, 8, 1)) <= TOL
 
 
-@pytest.mark.parametrize("T,chunk", [(3000, 16), (3000, 32), (3000, 48), (3000, 256), (3000, 4096), (5000, 16),
-                                     (1500, 16), (700, 16)])
+@pytest.mark.parametrize("T,chunk", [(3000, 16), (3000, 32), (3000, 48), (3000, 80), (3000, 256), (3000, 4096),
+                                     (5000, 16), (1500, 16), (700, 16), (4200, 0), (8300, 0), (12400, 0)])
 def test_decode_split_counts(ctx, T, chunk):
-    """Split-K partials merge to the same result for any split size: the
-    merge's shapes for 44, 47, 94, 188 and 313 splits (two batches), and
-    a single split."""
+    """Split-K partials merge to the same result for any split size (a
+    multiple of 16 keys, not only powers of two): the merge's shapes for 12
+    to 313 splits (two batches) and a single split; 0 = the automatic size,
+    which just past 256 x a power of two is no longer a power of two
+    (4200 keys: 32, 8300: 48, 12400: 64 keys per split)."""
     d = 512
     q, K, V, _ = I.decode_case(55 + T, T, d, True)
     ctx.set_decode_chunk(chunk)
@@ -274,7 +276,7 @@ def test_ragged_batch_shapes(ctx, name, lens, d, n_heads, n_kv):
     assert worst <= TOL
 
 
-@pytest.mark.parametrize("chunk", [64, 16])
+@pytest.mark.parametrize("chunk", [64, 16, 48, 80])
 def test_ragged_batch_with_set_split_size(ctx, chunk):
     """A split size set by the caller selects the per-sequence split grid;
     the merge folds 1 to 313 splits per sequence (at 16 keys: 94, 2, 21,

@@ -33,6 +33,7 @@ CASES = [  # d, attended rows, position of the last row, owner layer, KV heads
     (512, 4096, 4095, True, 1), (512, 1, 0, True, 1), (512, 40, 39, True, 1), (512, 64, 63, True, 1),
     (512, 65, 64, True, 1), (512, 9000, 8999, True, 1), (256, 512, 1200, True, 1), (256, 17, 16, True, 1),
     (256, 512, 700, False, 1), (512, 3000, 2999, False, 1), (512, 300, 299, True, 2), (256, 100, 99, False, 2),
+    (512, 8300, 8299, False, 1),  # 48-key splits: a context just past 256 x 32
 ]
 
 
