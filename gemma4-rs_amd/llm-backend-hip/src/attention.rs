@@ -230,7 +230,8 @@ impl HipPort {
         })
     }
 
-    /// Keys per split of the decode kernels (0: chosen per call).
+    /// Keys per split of the decode kernels, rounded up to a multiple of 16
+    /// (0: chosen per call).
     pub fn set_decode_chunk(&self, keys: usize) -> Result<(), EngError> {
         let keys = len_i64(keys)?;
         // SAFETY: ctx is live.
