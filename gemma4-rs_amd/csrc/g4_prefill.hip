@@ -1019,58 +1019,48 @@ __global__ __launch_bounds__(PrefillShape<D>::THREADS, 1) void prefill_kernel(Pr
     }
 }
 
-// Combines the units of one position block (and KV head) in key order for
+// Combines the NU units of one position block (and KV head) in key order for
 // the rows and dims of one producing wavefront (blockIdx.z), then writes
 // them row-major through LDS.  The per-unit loads of an element are
-// unrolled so that they are all in flight together.
-template <int D>
-__global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillK p) {
+// unrolled so that they are all in flight together; the unit count is a
+// template argument (the kernel switches on the block's count), so each
+// thread issues exactly its NU loads per element.
+template <int D, int NU>
+__device__ __forceinline__ void merge_units(const PrefillK &p, const PrefillBlockInfo &bi, float (*w)[kRowsPerWave],
+                                            float *Linv, float *tr) {
     using S = PrefillShape<D>;
     constexpr int DH = S::DH;
     constexpr int NT = DH / 16;
-    const PrefillBlockInfo bi = p.blocks[blockIdx.x];
-    if (bi.n_units <= 1) return;
     const int kvh = blockIdx.y, wave = blockIdx.z;
     const int rg = wave % kWaves, half = wave / kWaves;
     const int tid = threadIdx.x;
-    __shared__ float w[kPrefillMaxUnitsDev][kRowsPerWave];
-    __shared__ float Linv[kRowsPerWave];
-    __shared__ float tr[kRowsPerWave * DH];
-    const int n = bi.n_units;
     // Every load first (one memory round trip): the wave's (m, l) per row and
-    // unit, and this thread's partial vectors.  Units j >= n reload unit n-1
-    // (unconditional loads, no wait between them) and are zeroed when used.
+    // unit, and this thread's partial vectors.
     constexpr int NE = NT * 64 / 256;  // vectors per thread
     static_assert(NT * 64 % 256 == 0, "whole vectors per thread");
     const int row = rg * kRowsPerWave + (tid & (kRowsPerWave - 1));
-    float2 ml[kPrefillMaxUnitsDev];
+    float2 ml[NU];
 #pragma unroll
-    for (int j = 0; j < kPrefillMaxUnitsDev; ++j)
-        ml[j] = p.part_ml[((int64_t)(bi.first_slot + min(j, n - 1)) * gridDim.y + kvh) * 64 + row];
+    for (int j = 0; j < NU; ++j) ml[j] = p.part_ml[((int64_t)(bi.first_slot + j) * gridDim.y + kvh) * 64 + row];
     const int64_t slot_stride = (int64_t)gridDim.y * kWaves * kRowsPerWave * D / 4;  // f32x4
     const f32x4 *base = (const f32x4 *)p.part_o +
                         ((int64_t)bi.first_slot * gridDim.y + kvh) * (kWaves * kRowsPerWave * D / 4) +
                         (int64_t)wave * NT * 64;
-    f32x4 v[NE][kPrefillMaxUnitsDev];
+    f32x4 v[NE][NU];
 #pragma unroll
     for (int k = 0; k < NE; ++k)
 #pragma unroll
-        for (int j = 0; j < kPrefillMaxUnitsDev; ++j)
-            v[k][j] = base[min(j, n - 1) * slot_stride + tid + 256 * k];
+        for (int j = 0; j < NU; ++j) v[k][j] = base[j * slot_stride + tid + 256 * k];
     __builtin_amdgcn_sched_barrier(0);  // no wait before every load above is issued
     if (tid < kRowsPerWave) {
         float M = -INFINITY;
 #pragma unroll
-        for (int j = 0; j < kPrefillMaxUnitsDev; ++j)
-            if (j < n) M = fmaxf(M, ml[j].x);
+        for (int j = 0; j < NU; ++j) M = fmaxf(M, ml[j].x);
         float L = 0.0f;
 #pragma unroll
-        for (int j = 0; j < kPrefillMaxUnitsDev; ++j) {
-            float wj = 0.0f;
-            if (j < n) {
-                wj = ml[j].x == -INFINITY ? 0.0f : exp2_fast((ml[j].x - M) * kLog2e);
-                L += wj * ml[j].y;
-            }
+        for (int j = 0; j < NU; ++j) {
+            const float wj = ml[j].x == -INFINITY ? 0.0f : exp2_fast((ml[j].x - M) * kLog2e);
+            L += wj * ml[j].y;
             w[j][tid] = wj;
         }
         Linv[tid] = 1.0f / L;
@@ -1083,8 +1073,7 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillK p) {
         const int g = lane >> 4, c = lane & 15;
         f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int j = 0; j < kPrefillMaxUnitsDev; ++j)
-            acc += w[j][c] * (j < n ? v[k][j] : f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+        for (int j = 0; j < NU; ++j) acc += w[j][c] * v[k][j];
         const int U = tile >> 2, i = tile & 3;
         const float inv = Linv[c];
 #pragma unroll
@@ -1100,6 +1089,25 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillK p) {
             float *orow = p.out + ((rpos - p.pos0) * p.n_heads + kvh * kGroup + (row & 7)) * D + half * DH;
             *(f32x4 *)(orow + 4 * c4) = *(const f32x4 *)(tr + row * DH + 4 * c4);
         }
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillK p) {
+    __shared__ float w[kPrefillMaxUnitsDev][kRowsPerWave];
+    __shared__ float Linv[kRowsPerWave];
+    __shared__ float tr[kRowsPerWave * PrefillShape<D>::DH];
+    const PrefillBlockInfo bi = p.blocks[blockIdx.x];
+    static_assert(kPrefillMaxUnitsDev == 8, "one case per unit count");
+    switch (bi.n_units) {  // uniform; 0 or 1 unit: nothing to merge
+        case 2: merge_units<D, 2>(p, bi, w, Linv, tr); break;
+        case 3: merge_units<D, 3>(p, bi, w, Linv, tr); break;
+        case 4: merge_units<D, 4>(p, bi, w, Linv, tr); break;
+        case 5: merge_units<D, 5>(p, bi, w, Linv, tr); break;
+        case 6: merge_units<D, 6>(p, bi, w, Linv, tr); break;
+        case 7: merge_units<D, 7>(p, bi, w, Linv, tr); break;
+        case 8: merge_units<D, 8>(p, bi, w, Linv, tr); break;
+        default: break;
     }
 }
 
