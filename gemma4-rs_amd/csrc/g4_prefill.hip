@@ -329,6 +329,7 @@ struct PrefillLds {
     f32x4 *k0, *v0, *k1, *v1;
     f32x4 (*s0)[64], (*s1)[64];
     int *nf_tile;
+    int *vote;  // one word per wavefront: the split form's go / no-go
 };
 
 template <int D, bool SPLIT16>
@@ -427,20 +428,15 @@ __device__ __forceinline__ bool prefill_unit(const PrefillK &p, const PrefillUni
         for (int i = 0; i < 2 * PER_THREAD; ++i) issue_part(t, i, kb, vb);
     };
 
-    // The split form issues its first tiles before it knows whether it will
-    // use them, so that their latency overlaps the q loads and the check.
+    // The split form loads its tile flags and q first, then issues its first
+    // tiles before it knows whether it will use them: the flags and q land
+    // while the tiles are in flight, and the check below waits for them
+    // only (loads complete in order), not for the tiles.
+    int flags = 0;
     if constexpr (SPLIT16) {
-        // K(0), V(0) and K(1): the split form's step loop reads K one step
-        // ahead of V.
-#pragma unroll
-        for (int j = 0; j < TPS; ++j) {
-            issue_tile(u.t_lo + j < u.t_hi ? u.t_lo + j : u.t_hi - 1, lds_k0 + j * TILE_F4, lds_v0 + j * TILE_F4);
-            const int t1 = u.t_lo + TPS + j < u.t_hi ? u.t_lo + TPS + j : u.t_hi - 1;
-#pragma unroll
-            for (int e = 0; e < PER_THREAD; ++e) issue_part(t1, 2 * e, lds_k1 + j * TILE_F4, nullptr);
-        }
+        for (int f = 2 * u.t_lo + tid; f < 2 * u.t_hi; f += S::THREADS)  // (tile, K | V) flags
+            flags |= p.tile_flags[((int64_t)(f / 2 - p.t0) * gridDim.y + kvh) * 2 + (f & 1)];
     }
-
     // Q^T (B operand): lane (g, c) holds q[row c][d0 + 32u + 8g + j].
     float qreg[NU][8];
     {
@@ -455,6 +451,17 @@ __device__ __forceinline__ bool prefill_unit(const PrefillK &p, const PrefillUni
                 qreg[uu][j] = a[j];
                 qreg[uu][4 + j] = b[j];
             }
+        }
+    }
+    if constexpr (SPLIT16) {
+        // K(0), V(0) and K(1): the split form's step loop reads K one step
+        // ahead of V.
+#pragma unroll
+        for (int j = 0; j < TPS; ++j) {
+            issue_tile(u.t_lo + j < u.t_hi ? u.t_lo + j : u.t_hi - 1, lds_k0 + j * TILE_F4, lds_v0 + j * TILE_F4);
+            const int t1 = u.t_lo + TPS + j < u.t_hi ? u.t_lo + TPS + j : u.t_hi - 1;
+#pragma unroll
+            for (int e = 0; e < PER_THREAD; ++e) issue_part(t1, 2 * e, lds_k1 + j * TILE_F4, nullptr);
         }
     }
     // Split form: Q^T as hi and lo halves, in the same lanes.  The unit runs
@@ -473,9 +480,18 @@ __device__ __forceinline__ bool prefill_unit(const PrefillK &p, const PrefillUni
                 qh[uu][j] = h;
                 ql[uu][j] = lo;
             }
-        for (int f = 2 * u.t_lo + tid; f < 2 * u.t_hi; f += S::THREADS)  // (tile, K | V) flags
-            off |= p.tile_flags[((int64_t)(f / 2 - p.t0) * gridDim.y + kvh) * 2 + (f & 1)] != 0;
-        if (__syncthreads_or(off)) {
+        off |= flags != 0;
+        // Workgroup vote through LDS behind an LDS-only barrier (a
+        // __syncthreads would also wait for the tiles in flight).  The next
+        // vote's writes follow this unit's later barriers, so no wave
+        // overwrites a word another is still reading.
+        const bool any = __any(off);  // every lane takes part in the ballot
+        if (lane == 0) L.vote[wave] = any ? 1 : 0;
+        lds_barrier();
+        int v = 0;
+#pragma unroll
+        for (int w = 0; w < S::WAVES; ++w) v |= L.vote[w];
+        if (v != 0) {
             __builtin_amdgcn_s_waitcnt(kVmcntZero);
             return false;
         }
@@ -999,8 +1015,9 @@ __global__ __launch_bounds__(PrefillShape<D>::THREADS, 1) void prefill_kernel(Pr
     // fix-up pass; the unit's first barrier orders the clear before any
     // read.
     __shared__ int nf_tile[S::KSPLIT];
+    __shared__ int vote[S::WAVES];
     if (threadIdx.x < S::KSPLIT) nf_tile[threadIdx.x] = 0;
-    const PrefillLds L{lds_k0, lds_v0, lds_k1, lds_v1, lds_s0, lds_s1, nf_tile};
+    const PrefillLds L{lds_k0, lds_v0, lds_k1, lds_v1, lds_s0, lds_s1, nf_tile, vote};
     // Workgroups go to the 8 XCDs round-robin (workgroup w to XCD w % 8).
     // Bin b runs on XCD b / (bins / 8), so that consecutive bins -- the
     // schedule lists a sliding layer's blocks in position order -- share
