@@ -547,9 +547,7 @@ struct PairPipe {
     __device__ __forceinline__ void load_pair(const DecodeLane<D> &ln, __amdgpu_buffer_rsrc_t krs,
                                               __amdgpu_buffer_rsrc_t vrs, int q_first, int n_pairs, int i,
                                               KvTile<D> (&P)[2]) const {
-        // A pair past the run's last reads zeros from past the resources'
-        // range (no memory request), the loads themselves unconditional.
-        const int q = q_first + i;
+        const int q = q_first + (i < n_pairs ? i : n_pairs - 1);
         ln.template load_tile<AUX>(krs, vrs, 2 * q, P[0]);
         ln.template load_tile<AUX>(krs, vrs, 2 * q + 1, P[1]);
     }
