@@ -740,50 +740,59 @@ __device__ __forceinline__ bool prefill_unit(const PrefillK &p, const PrefillUni
     if constexpr (SPLIT16) {
         // Software pipeline over steps s of TPS tiles: K(s) in k[s % 2], V(s)
         // in v[s % 2], K loaded one step ahead of V.  Iteration s, after the
-        // step's one barrier: step s's full scores (the pair's partials,
-        // written at the end of iteration s-1), its mask, maximum and lazy
-        // rescale; then, in one straight-line block, the score MFMAs of step
-        // s+1 with the next loads and step s's weights (VALU) between them,
-        // and P.V(s); last, step s+1's partial scores go to the exchange slot
-        // that the next barrier publishes.  The two waves of a SIMD (the
-        // pair, at D = 512) thus no longer stop for a mid-step exchange, and
-        // the softmax runs beside the matrix pipe.
+        // step's one barrier: the first half of step s+1's score MFMAs (with
+        // half of the next loads), and beside them step s's full scores (the
+        // pair's partials, written at the end of iteration s-1), mask and
+        // row maximum, which those MFMAs do not wait for; the lazy rescale;
+        // the second half of the score MFMAs with step s's weights (VALU)
+        // between them; P.V(s); last, step s+1's partial scores go to the
+        // exchange slot that the next barrier publishes.  So the matrix pipe
+        // starts right after the barrier instead of after the softmax's
+        // dependent chain, and the two waves of a SIMD (the pair, at
+        // D = 512) do not stop for a mid-step exchange.
         const int nsteps = (u.t_hi - u.t_lo + TPS - 1) / TPS;
         auto tile_at = [&](int st, int j) {
             const int tt = u.t_lo + TPS * st + j;
             return tt < u.t_hi ? tt : u.t_hi - 1;  // past the end: the last tile again (unread)
         };
-        // Partial S^T of step st's tile for this wave's group over its dims,
-        // from kt (that step's K buffer); load(i) for i < NL spread over the
-        // chunks.  A stale tile (past the unit) is computed anyway, from the
-        // finite values its buffer holds, and masked whole.
+        // Partial S^T of a step's tile for this wave's group over its dims,
+        // from kt (that step's K buffer), one 32-dim chunk at a time; the
+        // step's NL tile-part loads, load(i), are spread over the chunks.  A
+        // stale tile (past the unit) is computed anyway, from the finite
+        // values its buffer holds, and masked whole.
         constexpr int NL = 2 * PER_THREAD * TPS;  // tile-part loads per step
         static_assert(NL % NU == 0 || NU % NL == 0, "loads spread over the chunks");
+        auto read_k = [&](const f32x4 *kt, int uu, f32x4(&dst)[2]) {
+            const int ug = d0 / 32 + uu;
+            dst[0] = kt[(ug * 2 + 0) * 64 + lane];
+            dst[1] = kt[(ug * 2 + 1) * 64 + lane];
+        };
+        // Chunk uu: its three MFMAs into a0..a2 from the K operands in
+        // kc[uu & 1], after chunk uu+1's operands are read into the other slot
+        // and the chunk's share of the loads is issued.
+        auto score_chunk = [&](const f32x4 *kt, int uu, f32x4(&kc)[2][2], f32x4 &a0, f32x4 &a1, f32x4 &a2,
+                               auto &&load) {
+            if (uu + 1 < NU) read_k(kt, uu + 1, kc[(uu + 1) & 1]);
+            if constexpr (NL >= NU) {
+#pragma unroll
+                for (int i = uu * (NL / NU); i < (uu + 1) * (NL / NU); ++i) load(i);
+            } else if (uu % (NU / NL) == 0) {
+                load(uu / (NU / NL));
+            }
+            const f16x8 kh = __builtin_bit_cast(f16x8, kc[uu & 1][0]);
+            const f16x8 kl = __builtin_bit_cast(f16x8, kc[uu & 1][1]);
+            a0 = split_mfma(kh, qh[uu], a0);
+            a1 = split_mfma(kh, ql[uu], a1);
+            a2 = split_mfma(kl, qh[uu], a2);
+        };
+        // All chunks of one tile (the unit's first step).
         auto part_scores = [&](const f32x4 *kb_, auto &&load) -> f32x4 {
             const f32x4 *kt = kb_ + kpar * TILE_F4;
             f32x4 a0 = {0.0f, 0.0f, 0.0f, 0.0f}, a1 = a0, a2 = a0;
             f32x4 kc[2][2];
-            auto read_k = [&](int uu, f32x4(&dst)[2]) {
-                const int ug = d0 / 32 + uu;
-                dst[0] = kt[(ug * 2 + 0) * 64 + lane];
-                dst[1] = kt[(ug * 2 + 1) * 64 + lane];
-            };
-            read_k(0, kc[0]);
+            read_k(kt, 0, kc[0]);
 #pragma unroll
-            for (int uu = 0; uu < NU; ++uu) {
-                if (uu + 1 < NU) read_k(uu + 1, kc[(uu + 1) & 1]);
-                if constexpr (NL >= NU) {
-#pragma unroll
-                    for (int i = uu * (NL / NU); i < (uu + 1) * (NL / NU); ++i) load(i);
-                } else if (uu % (NU / NL) == 0) {
-                    load(uu / (NU / NL));
-                }
-                const f16x8 kh = __builtin_bit_cast(f16x8, kc[uu & 1][0]);
-                const f16x8 kl = __builtin_bit_cast(f16x8, kc[uu & 1][1]);
-                a0 = split_mfma(kh, qh[uu], a0);
-                a1 = split_mfma(kh, ql[uu], a1);
-                a2 = split_mfma(kl, qh[uu], a2);
-            }
+            for (int uu = 0; uu < NU; ++uu) score_chunk(kt, uu, kc, a0, a1, a2, load);
             return a0 + (a1 + a2) * kLoUnscale;
         };
         // K(0), V(0) and K(1) were issued at the unit's start.
@@ -804,31 +813,58 @@ __device__ __forceinline__ bool prefill_unit(const PrefillK &p, const PrefillUni
                         f32x4(*xw)[64]) {
             __builtin_amdgcn_s_waitcnt(kVmcntZero);
             __syncthreads();  // K(st+1), V(st) and step st's partials are in; k(st), v(st-1) are free
+            auto load = [&](int i) {
+                const int j = i / (2 * PER_THREAD), part = i % (2 * PER_THREAD);
+                if (part & 1)
+                    issue_part(tile_at(st + 1, j), part, nullptr, vnext + j * TILE_F4);
+                else
+                    issue_part(tile_at(st + 2, j), part, kfree + j * TILE_F4, nullptr);
+            };
+            // First half of step st+1's score MFMAs, with step st's full
+            // scores, mask and row maximum found beside them (none of which
+            // they depend on).
+            const f32x4 *kt = kn1 + kpar * TILE_F4;
+            f32x4 a0 = {0.0f, 0.0f, 0.0f, 0.0f}, a1 = a0, a2 = a0;
+            f32x4 kc[2][2];
+            read_k(kt, 0, kc[0]);
             f32x4 sc;
             if constexpr (S::SPLIT == 2)
                 sc = xr[rg][lane] + xr[rg + kWaves][lane];  // half 0 + half 1, in that order
             else
                 sc = sc_next;
+            constexpr int H = NU / 2;
+#pragma unroll
+            for (int uu = 0; uu < H; ++uu) score_chunk(kt, uu, kc, a0, a1, a2, load);
             const int tw = u.t_lo + TPS * st + kpar;
             const bool live = S::KSPLIT == 1 || tw < u.t_hi;
+            // Key 4g + r of the tile is kept iff the tile is live and every
+            // row attends it whole, or key <= pos and, with a window,
+            // key > pos - W (branch-free).
+            const bool ex = exact(tw);
+            const int64_t rel = pos - 16LL * tw;
+            const int64_t rlo = rel - win;
             float sv[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) sv[r] = scaled ? sc[r] * p.scale : sc[r];
-            if (!live) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) sv[r] = -INFINITY;
-            } else if (!exact(tw)) {
-                const int64_t rel = pos - 16LL * tw;  // key - 16tw <= rel, and > rel - win
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int kr = 4 * g + r;
-                    if (!(kr <= rel && (win == 0 || kr > rel - win))) sv[r] = -INFINITY;
-                }
+            for (int r = 0; r < 4; ++r) {
+                const int kr = 4 * g + r;
+                const bool keep = live & (ex | ((kr <= rel) & ((win == 0) | (kr > rlo))));
+                sv[r] = keep ? sc[r] * p.scale : -INFINITY;  // x * 1 == x
             }
             const float mx = __builtin_elementwise_maximum(__builtin_elementwise_maximum(sv[0], sv[1]),
                                                            __builtin_elementwise_maximum(sv[2], sv[3]));
             bad |= __builtin_amdgcn_classf(mx, 0x203);  // signalling/quiet NaN, +inf
             const float mt = rows_max(mx);
+            // Order: chunk 0's K reads (and the partials); per chunk the next
+            // chunk's K reads, its share of the loads, its three MFMAs and
+            // some of the VALU above.
+            __builtin_amdgcn_sched_group_barrier(0x100, S::SPLIT == 2 ? 4 : 2, 0);  // DS read
+#pragma unroll
+            for (int uu = 0; uu < H; ++uu) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);                        // DS read
+                __builtin_amdgcn_sched_group_barrier(0x010, NL >= NU ? NL / NU : 1, 0);  // VMEM
+                __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);                        // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);                        // VALU
+            }
             if (__any(mt > m + kRescaleSlackSplit)) {
                 const float m_new = fmaxf(m, mt);
                 const float alpha = (m_new == -INFINITY) ? 1.0f : exp2_fast((m - m_new) * kLog2e);
@@ -837,16 +873,10 @@ __device__ __forceinline__ bool prefill_unit(const PrefillK &p, const PrefillUni
 #pragma unroll
                 for (int i = 0; i < NT; ++i) o[i] *= alpha;
             }
-            // One straight-line block from here: the score MFMAs of step
-            // st+1 with this iteration's loads, step st's weights, P.V(st).
-            auto load = [&](int i) {
-                const int j = i / (2 * PER_THREAD), part = i % (2 * PER_THREAD);
-                if (part & 1)
-                    issue_part(tile_at(st + 1, j), part, nullptr, vnext + j * TILE_F4);
-                else
-                    issue_part(tile_at(st + 2, j), part, kfree + j * TILE_F4, nullptr);
-            };
-            const f32x4 part = part_scores(kn1, load);
+            // Second half of the score MFMAs, with step st's weights.
+#pragma unroll
+            for (int uu = H; uu < NU; ++uu) score_chunk(kt, uu, kc, a0, a1, a2, load);
+            const f32x4 part = a0 + (a1 + a2) * kLoUnscale;
             float pr[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r)
@@ -862,6 +892,18 @@ __device__ __forceinline__ bool prefill_unit(const PrefillK &p, const PrefillUni
                 pl[r] = lo;
                 pl[4 + r] = lo;
             }
+            // The same order for the second half, with the weights' VALU.
+#pragma unroll
+            for (int uu = H; uu < NU; ++uu) {
+                if (uu + 1 < NU) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);       // DS read
+                __builtin_amdgcn_sched_group_barrier(0x010, NL >= NU ? NL / NU : 1, 0);  // VMEM
+                __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);                        // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);                        // VALU
+            }
+            // P.V is scheduled as a region of its own: scheduled together
+            // with the score MFMAs, the first of the two unrolled iterations
+            // read each V operand just before its MFMAs and waited for it.
+            __builtin_amdgcn_sched_barrier(0);
             // P.V(st); a stale tile's weights are 0 and its V is finite.
             static_assert(NT % 2 == 0, "O^T tiles in pairs");
             const f32x4 *vt = vcur + kpar * TILE_F4 + (d0 / 16) * 64 + lane;
@@ -875,34 +917,25 @@ __device__ __forceinline__ bool prefill_unit(const PrefillK &p, const PrefillUni
                     vc[sl ^ 1][0] = vt[(T + 2) * 64];
                     vc[sl ^ 1][1] = vt[(T + 3) * 64];
                 }
-                const f16x8 a0 = __builtin_bit_cast(f16x8, vc[sl][0]);
-                const f16x8 a1 = __builtin_bit_cast(f16x8, vc[sl][1]);
-                o[T] = split_mfma(a0, ph, o[T]);
-                o[T + 1] = split_mfma(a1, ph, o[T + 1]);
-                o[T] = split_mfma(a0, pl, o[T]);
-                o[T + 1] = split_mfma(a1, pl, o[T + 1]);
+                const f16x8 a0v = __builtin_bit_cast(f16x8, vc[sl][0]);
+                const f16x8 a1v = __builtin_bit_cast(f16x8, vc[sl][1]);
+                o[T] = split_mfma(a0v, ph, o[T]);
+                o[T + 1] = split_mfma(a1v, ph, o[T + 1]);
+                o[T] = split_mfma(a0v, pl, o[T]);
+                o[T + 1] = split_mfma(a1v, pl, o[T + 1]);
             }
             if constexpr (S::SPLIT == 2)
                 xw[wave][lane] = part;
             else
                 sc_next = part;
-            // Order: K reads of chunk 0; per chunk the next chunk's K reads,
-            // its share of the loads, its three MFMAs and a few VALU of the
-            // weights; then P.V, two V reads per four MFMAs.
-            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
-#pragma unroll
-            for (int uu = 0; uu < NU; ++uu) {
-                if (uu + 1 < NU) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);       // DS read
-                __builtin_amdgcn_sched_group_barrier(0x010, NL >= NU ? NL / NU : 1, 0);  // VMEM
-                __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);                        // MFMA
-                __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);                        // VALU
-            }
+            // P.V: two V reads per four MFMAs.
             __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
 #pragma unroll
             for (int T = 0; T < NT; T += 2) {
                 if (T + 2 < NT) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
                 __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);                   // MFMA
             }
+            __builtin_amdgcn_sched_barrier(0);  // the next iteration's barrier stays after this P.V
         };
         int st = 0;
         for (; st + 1 < nsteps; st += 2) {
