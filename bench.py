@@ -532,6 +532,7 @@ def floors_lib():
     lib.g4f_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
     lib.g4f_mfma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
     lib.g4f_lds_mfma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    lib.g4f_mix.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
     return lib
 
 
@@ -542,7 +543,9 @@ def bench_floors(torch, steps, warmup):
     layer's K/V, resident), 16 MiB (a 4096-key global layer's, HBM-cold:
     copies rotated), 32 MiB (about the ragged batch's 32 sliding windows,
     resident in the Infinity Cache) and 1 GiB (HBM-cold by size), each one
-    launch of 2048 x 256 threads with 16-byte non-temporal loads."""
+    launch of 2048 x 256 threads with 16-byte non-temporal loads; and the
+    matrix-pipe rates the prefill kernels are read against: MFMAs alone, fed
+    from LDS, and beside independent VALU work."""
     lib = floors_lib()
 
     def check(rc):
@@ -597,6 +600,23 @@ def bench_floors(torch, steps, warmup):
             if mpr:
                 r["lds_bytes_per_clk_per_cu"] = round(4 * wps * 8 * lit * 1024 / (s * 2.4e9), 1)
             res[f"lds_fed_mfma_{shape}_{mpr}_per_read_{wps}_waves_per_simd"] = r
+    # MFMA / VALU overlap (g4f_mix): one workgroup of eight waves per CU; an
+    # MFMA wave issues 4 x mit 16x16x32 f16 MFMAs, an FMA wave 16 x mit f32
+    # FMAs, an interleaving wave k FMAs after each of its 4 x mit MFMAs.
+    mit = 4096
+    for name, mode, k in (("mfma_2_waves_per_simd", 0, 1), ("mfma_1_wave_per_simd", 1, 1),
+                          ("fma_1_wave_per_simd", 2, 1), ("mfma_wave_and_fma_wave_per_simd", 3, 1),
+                          ("interleaved_1_fma_per_mfma_1_wave", 4, 1), ("interleaved_2_fma_per_mfma_1_wave", 4, 2),
+                          ("interleaved_4_fma_per_mfma_1_wave", 4, 4), ("interleaved_1_fma_per_mfma_2_waves", 5, 1),
+                          ("interleaved_2_fma_per_mfma_2_waves", 5, 2), ("interleaved_4_fma_per_mfma_2_waves", 5, 4)):
+        wall, ev = time_steps(torch, lambda i: check(lib.g4f_mix(mode, k, 256, mit, msink.data_ptr(), stream())),
+                              lsteps, 1)
+        s = ev / lsteps
+        mfma_per_simd = 4 * mit * (2 if mode in (0, 5) else 0 if mode == 2 else 1)
+        r = {"us": round(s * 1e6, 2)}
+        if mfma_per_simd:
+            r["cycles_per_mfma_at_2400mhz"] = round(s * 2.4e9 / mfma_per_simd, 2)
+        res[f"overlap_{name}"] = r
     del msink
     torch.cuda.empty_cache()
     return res

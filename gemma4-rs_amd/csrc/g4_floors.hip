@@ -9,7 +9,10 @@
 //    accumulators per wave, as many waves per SIMD as asked;
 //  - the matrix pipe fed from LDS: one 16-byte operand per lane read from
 //    LDS per one or two MFMAs (16x16x32 or 32x32x16 f16), which bounds what
-//    a kernel streaming its operands through LDS can keep busy.
+//    a kernel streaming its operands through LDS can keep busy;
+//  - MFMA / VALU overlap: how much independent f32 FMA work runs beside the
+//    16x16x32 f16 MFMAs, from another wave of the same SIMD or from the same
+//    wave between its MFMAs.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -117,6 +120,84 @@ __global__ __launch_bounds__(256) void lds_mfma_kernel(float *sink, int iters) {
     sink[blockIdx.x * 256 + threadIdx.x] = s;
 }
 
+// MFMA / VALU overlap on workgroups of eight waves (waves w and w + 4 share
+// a SIMD), one workgroup per CU (the LDS array reserves most of a CU's LDS).
+// A wave of MFMAs runs `iters` rounds of four independent MFMAs; a wave of
+// FMAs `iters` rounds of sixteen FMAs on eight independent chains (nominally
+// as many VALU cycles as the MFMAs' 64 matrix cycles); an interleaving wave
+// K FMAs after each of its MFMAs.  MODE: 0 every wave MFMAs; 1 waves 0-3
+// MFMAs, the rest idle; 2 waves 4-7 FMAs, the rest idle; 3 waves 0-3 MFMAs
+// and waves 4-7 FMAs; 4 waves 0-3 interleave, the rest idle; 5 every wave
+// interleaves.
+template <int MODE, int K>
+__global__ __launch_bounds__(512) void mix_kernel(float *sink, int iters, float fa, float fb) {
+    __shared__ float pad[24 * 1024];
+    const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
+    if (threadIdx.x == 0) pad[0] = fa;
+    f16x8 a, b;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        a[j] = (_Float16)(l * 0.001f + j);
+        b[j] = (_Float16)(j * 0.5f);
+    }
+    f32x4 c0 = {0.0f, 0.0f, 0.0f, 0.0f}, c1 = c0, c2 = c0, c3 = c0;
+    float x[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = l * 0.01f + i;
+    const bool first = wave < 4;
+    const bool mfma = MODE == 0 || ((MODE == 1 || MODE == 3) && first);
+    const bool fma = (MODE == 2 || MODE == 3) && !first;
+    const bool mixed = MODE == 5 || (MODE == 4 && first);
+    if (mfma) {
+        for (int it = 0; it < iters; ++it) {
+            c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c0, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c1, 0, 0, 0);
+            c2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c2, 0, 0, 0);
+            c3 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c3, 0, 0, 0);
+        }
+    }
+    if (fma) {
+        for (int it = 0; it < iters; ++it) {
+#pragma unroll
+            for (int r = 0; r < 2; ++r)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) x[i] = __builtin_fmaf(x[i], fa, fb);
+        }
+    }
+    if (mixed) {
+        for (int it = 0; it < iters; ++it) {
+            c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c0, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < K; ++i) x[i & 7] = __builtin_fmaf(x[i & 7], fa, fb);
+            c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c1, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < K; ++i) x[(i + 2) & 7] = __builtin_fmaf(x[(i + 2) & 7], fa, fb);
+            c2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c2, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < K; ++i) x[(i + 4) & 7] = __builtin_fmaf(x[(i + 4) & 7], fa, fb);
+            c3 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c3, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < K; ++i) x[(i + 6) & 7] = __builtin_fmaf(x[(i + 6) & 7], fa, fb);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, K, 0);  // VALU
+            }
+        }
+    }
+    const f32x4 s = (c0 + c1) + (c2 + c3);
+    float t = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) t += x[i];
+    __syncthreads();
+    sink[blockIdx.x * 512 + threadIdx.x] = (s[0] + s[1]) + (s[2] + s[3]) + t + pad[l];
+}
+
+template <int MODE, int K>
+void launch_mix(int grid, int iters, float *sink, hipStream_t st) {
+    hipLaunchKernelGGL((mix_kernel<MODE, K>), dim3((unsigned)grid), dim3(512), 0, st, sink, iters, 1.0001f, 0.5f);
+}
+
 }  // namespace
 
 extern "C" {
@@ -165,6 +246,31 @@ int g4f_lds_mfma(int mode, int grid, int iters, float *sink, void *stream) {
         case 3: hipLaunchKernelGGL((lds_mfma_kernel<true, 0>), g, b, 0, st, sink, iters); break;
         case 4: hipLaunchKernelGGL((lds_mfma_kernel<true, 1>), g, b, 0, st, sink, iters); break;
         default: hipLaunchKernelGGL((lds_mfma_kernel<true, 2>), g, b, 0, st, sink, iters); break;
+    }
+    return hipGetLastError() == hipSuccess ? 0 : 1;
+}
+
+// One launch of the MFMA / VALU overlap kernel in `mode` (0..5, see
+// mix_kernel) with k (1, 2 or 4) FMAs per MFMA for the interleaving modes;
+// grid workgroups of eight waves, one per CU.  sink holds grid * 512 floats.
+int g4f_mix(int mode, int k, int grid, int iters, float *sink, void *stream) {
+    if (!sink || grid <= 0 || iters <= 0 || mode < 0 || mode > 5 || (k != 1 && k != 2 && k != 4)) return 1;
+    hipStream_t st = (hipStream_t)stream;
+    switch (mode) {
+        case 0: launch_mix<0, 1>(grid, iters, sink, st); break;
+        case 1: launch_mix<1, 1>(grid, iters, sink, st); break;
+        case 2: launch_mix<2, 1>(grid, iters, sink, st); break;
+        case 3: launch_mix<3, 1>(grid, iters, sink, st); break;
+        case 4:
+            if (k == 1) launch_mix<4, 1>(grid, iters, sink, st);
+            else if (k == 2) launch_mix<4, 2>(grid, iters, sink, st);
+            else launch_mix<4, 4>(grid, iters, sink, st);
+            break;
+        default:
+            if (k == 1) launch_mix<5, 1>(grid, iters, sink, st);
+            else if (k == 2) launch_mix<5, 2>(grid, iters, sink, st);
+            else launch_mix<5, 4>(grid, iters, sink, st);
+            break;
     }
     return hipGetLastError() == hipSuccess ? 0 : 1;
 }
