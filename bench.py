@@ -186,6 +186,31 @@ def bench_global_decode(ctx, torch, prep, steps, warmup, T=4096, d=512):
             "cache": f"HBM-cold: {min(copies, steps)} K/V copies of {per_copy >> 20} MiB rotated", "host": host}
 
 
+def bench_host_attend(ctx, torch, prep, steps, warmup=3):
+    """g4_attend, the form of `attend` over host buffers (model.rs:348-366
+    takes slices): per call it allocates device buffers, copies q, K and V
+    in, decodes, copies the output back and frees.  Timed on the host clock
+    around whole calls, at the shapes of the 64-key sliding decode and the
+    4096-key global decode; the rate counts the bytes that cross PCIe."""
+    res = {}
+    for name, T, d, base, glob in (("sliding_d256_ctx64", 64, 256, LOCAL_BASE, False),
+                                   ("global_d512_ctx4096", 4096, 512, GLOBAL_BASE, True)):
+        freqs = prep.rope_freqs(d) if glob else None
+        K = prep.rows(T, d, 0, base, freqs).cpu().numpy()
+        V = prep.rows(T, d, 0, 0.0, None, rope=False).cpu().numpy()
+        q = prep.rows(1, d, T - 1, base, freqs, heads=N_HEADS).cpu().numpy()
+        for _ in range(warmup):
+            ctx.attend(q, K, V, N_HEADS, N_KV)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            ctx.attend(q, K, V, N_HEADS, N_KV)
+        s = (time.perf_counter() - t0) / steps
+        nbytes = (2 * q.size + K.size + V.size) * 4
+        res[name] = {"us_per_call": round(s * 1e6, 1), "pcie_bytes": nbytes, "gbs": round(nbytes / s / 1e9, 3),
+                     "note": "host buffers in and out (pageable), device buffers allocated and freed per call"}
+    return res
+
+
 def stack_plan(g4hip, ctx_len):
     """The E2B stack's per-layer (source layer, kv range, head_dim, global)."""
     n_layers, shared = 35, 20
@@ -915,7 +940,7 @@ def cpu_ragged(cpu, host, nbytes, seconds):
 
 # ------------------------------------------------------------------ main
 ONLY = ["sliding", "global", "stack", "stackwarm", "layerstack", "prefill", "chunks", "ragged", "layer", "matvec",
-        "floors", "copy"]
+        "floors", "copy", "host"]
 
 
 def run_only(args, torch, g4hip):
@@ -933,6 +958,7 @@ def run_only(args, torch, g4hip):
               "chunks": lambda: bench_prefill_chunks(ctx, torch, prep, 10, 3),
               "matvec": lambda: bench_matvec(ctx, torch, max(20, k // 2), args.warmup),
               "floors": lambda: bench_floors(torch, max(20, k), 5),
+              "host": lambda: bench_host_attend(ctx, torch, prep, 20),
               "copy": lambda: bench_copy(torch, max(5, k // 4))}[args.only]
         res = fn()
         res.pop("host", None)
@@ -984,7 +1010,8 @@ def main():
         workloads = {"layer_drivers": bench_layer_steps(ctx, torch, prep, steps, warmup),
                      "prefill_long_context": bench_prefill_chunks(ctx, torch, prep, 10, 3),
                      "q8_0_matvec": bench_matvec(ctx, torch, max(20, k // 2), warmup),
-                     "floors": bench_floors(torch, k, 5)}
+                     "floors": bench_floors(torch, k, 5),
+                     "host_buffer_attend": bench_host_attend(ctx, torch, prep, 20)}
     cpu = {}
     if want:
         timer = CpuTimer()
