@@ -25,11 +25,11 @@ def dev(a):
     return torch.from_numpy(np.ascontiguousarray(a)).cuda()
 
 
-def run(ctx, q, K, V, pos0, N, window, d, exact):
+def run(ctx, q, K, V, pos0, N, window, d, exact, scale=1.0):
     ctx.set_prefill_exact(exact)
     try:
         out = torch.zeros(N * 8 * d, device="cuda")
-        ctx.attend_prefill(dev(q), dev(K), dev(V), pos0, N, window, 8, 1, d, out)
+        ctx.attend_prefill(dev(q), dev(K), dev(V), pos0, N, window, 8, 1, d, out, scale=scale)
         ctx.check_status()
         return out.cpu().numpy().reshape(N, 8 * d)
     finally:
@@ -45,14 +45,43 @@ def case(seed, rows, d):
     return q, K, V
 
 
-def worst_vs_oracle(got, q, K, V, pos0, window, unit=1.0):
+def worst_vs_oracle(got, q, K, V, pos0, window, unit=1.0, scale=1.0):
     """Worst rel_err over all rows, both sides divided by `unit` (the
     magnitude of V, so that the measure's floor of 1 does not hide errors
     of small outputs)."""
-    ref, status = orc.attend_prefill(q, K, V, pos0, window, 8, 1)
+    ref, status = orc.attend_prefill(q, K, V, pos0, window, 8, 1, scale=scale)
     assert not status.any()
     assert np.all(np.isfinite(got))
     return max(I.rel_err(got[i] / unit, ref[i] / unit) for i in range(ref.shape[0]))
+
+
+@pytest.mark.parametrize("scale", [0.0625, 2.5])
+@pytest.mark.parametrize("d,window,pos0,N", [(256, 512, 600, 128), (512, 0, 300, 96), (256, 8, 5, 40)])
+def test_softmax_scale(ctx, d, window, pos0, N, scale):
+    """A score scale other than Gemma's 1 (attend's `scale`, model.rs:326-343):
+    both forms against the oracle's token loop with the same scale, within
+    1e-4 or -- where larger scores put the reference's own f32 rounding
+    near that -- no further from exact (f64) attention than twice the
+    oracle's own distance from it (the bar of the large-score tests)."""
+    from test_gpu_prefill_deep import f64_prefill
+
+    print(f"[case] d={d} W={window} pos0={pos0} N={N} scale={scale}", flush=True)
+    q, K, V = case(7700 + d + pos0 + N, pos0 + N, d)
+    ref, status = orc.attend_prefill(q[pos0:], K, V, pos0, window, 8, 1, scale=scale)
+    assert not status.any()
+    exact64 = f64_prefill(q[pos0:].astype(np.float64) * scale, K, V, pos0, window)
+    floor = max(I.rel_err(ref[i], exact64[i]) for i in range(N))
+    for form, ex in (("split-f16", 0), ("f32", 1)):
+        got = run(ctx, q[pos0:], K, V, pos0, N, window, d, ex, scale)
+        assert np.all(np.isfinite(got))
+        w_ref = max(I.rel_err(got[i], ref[i]) for i in range(N))
+        w_64 = max(I.rel_err(got[i], exact64[i]) for i in range(N))
+        print(f"[parity] scale {scale} {form}: vs oracle {w_ref:.2e}, vs f64 {w_64:.2e}; oracle vs f64 {floor:.2e}",
+              flush=True)
+        assert w_ref <= TOL or w_64 <= 2.0 * floor, form
+    split = run(ctx, q[pos0:], K, V, pos0, N, window, d, 0, scale)
+    # The scale reached the kernels: the unscaled outputs differ.
+    assert not np.allclose(split, run(ctx, q[pos0:], K, V, pos0, N, window, d, 0), rtol=1e-3, atol=1e-3)
 
 
 @pytest.mark.parametrize("d,window,pos0,N", [(256, 512, 0, 2048), (512, 0, 0, 2048), (256, 512, 3000, 256),
