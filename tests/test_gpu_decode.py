@@ -276,6 +276,31 @@ def test_ragged_batch_shapes(ctx, name, lens, d, n_heads, n_kv):
     assert worst <= TOL
 
 
+@pytest.mark.parametrize("name,lens,d", [
+    ("stream", [16, 48, 80, 40000, 17, 31, 33], 512),
+    ("split", [5, 40, 700], 256),
+])
+def test_ragged_batch_softmax_scale(ctx, name, lens, d):
+    """attend's score scale (model.rs:326-343) through the batched forms:
+    the stream-K kernel (a batch with a 40000-key sequence) and the split
+    grid, against the oracle with the same scale."""
+    print(f"[case] ragged {name} d={d} scale 0.3", flush=True)
+    lens = np.array(lens, np.int64)
+    q, K, V, row0 = _ragged_case(len(lens) * 11 + d, lens, d)
+    B = len(lens)
+    out = torch.zeros(B * 8 * d, device="cuda")
+    ctx.attend_decode_batch(dev(q), dev(K), dev(V), dev(row0), dev(np.zeros(B, np.int64)), dev(lens), int(lens.max()),
+                            8, 1, d, out, scale=0.3)
+    ctx.check_status()
+    got = out.cpu().numpy().reshape(B, -1)
+    worst = 0.0
+    for s in range(B):
+        rows = slice(row0[s], row0[s] + lens[s])
+        worst = max(worst, I.rel_err(got[s], orc.attend(q[s], K[rows], V[rows], 8, 1, scale=0.3)))
+    print(f"[parity] ragged {name} scale 0.3: worst rel err {worst:.2e}")
+    assert worst <= TOL
+
+
 @pytest.mark.parametrize("chunk", [64, 16, 48, 80])
 def test_ragged_batch_with_set_split_size(ctx, chunk):
     """A split size set by the caller selects the per-sequence split grid;
