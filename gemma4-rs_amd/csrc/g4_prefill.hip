@@ -1088,10 +1088,10 @@ __device__ __forceinline__ void merge_units(const PrefillK &p, const PrefillBloc
     // unit, and this thread's partial vectors.
     constexpr int NE = NT * 64 / 256;  // vectors per thread
     static_assert(NT * 64 % 256 == 0, "whole vectors per thread");
-    const int row = rg * kRowsPerWave + (tid & (kRowsPerWave - 1));
+    const int ml_row = rg * kRowsPerWave + (tid & (kRowsPerWave - 1));
     float2 ml[NU];
 #pragma unroll
-    for (int j = 0; j < NU; ++j) ml[j] = p.part_ml[((int64_t)(bi.first_slot + j) * gridDim.y + kvh) * 64 + row];
+    for (int j = 0; j < NU; ++j) ml[j] = p.part_ml[((int64_t)(bi.first_slot + j) * gridDim.y + kvh) * 64 + ml_row];
     const int64_t slot_stride = (int64_t)gridDim.y * kWaves * kRowsPerWave * D / 4;  // f32x4
     const f32x4 *base = (const f32x4 *)p.part_o +
                         ((int64_t)bi.first_slot * gridDim.y + kvh) * (kWaves * kRowsPerWave * D / 4) +
